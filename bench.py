@@ -1,0 +1,234 @@
+"""Benchmark of the quantized DiT-block hot path on one MI355X.
+
+Workloads (synthetic, seeded, generated on the CPU then resident in HBM):
+  * W8A8 MLP at the 720p shape: M=25200 tokens, 5120 -> 13824 -> 5120,
+    y = fc2(gelu_tanh(fc1(x))) with per-token int8 activations -- `value`
+    (whole-job int8 TOPS, 4*M*d*ffn ops per step, quant/GELU/requant time
+    included);
+  * fused AdaLN-RMSNorm + 3D RoPE of Q and K at M=25200, d=5120 (40 x 128),
+    reported as HBM GB/s on 8*M*d algorithmic bytes.
+
+A step is one pass of the MLP block over the batch. The timed region runs the
+four MLP kernels (per-token quant, fc1 GEMM + dequant/GELU/row-amax epilogue,
+requant, fc2 GEMM + dequant) through the C ABI on torch's current stream, with
+HIP events between them, so per-kernel durations come from the same region.
+The CPU baseline is the oracle (torch-CPU restatement of the reference's eager
+path) on a bounded row sample, run on this host's cores.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POP/s
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_baseline_mlp(inp: dict, sample_rows: int, repeats: int = 3) -> dict:
+    import torch
+
+    from oracle import cpu_ref
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    x = inp["x"][:sample_rows]
+    args = (inp["w1"], inp["s1"], inp["w2"], inp["s2"])
+    cpu_ref.w8a8_mlp(x[:64], *args)          # warm-up
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        cpu_ref.w8a8_mlp(x, *args)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    d, f = inp["x"].shape[1], inp["w1"].shape[0]
+    return {"value": round(4.0 * sample_rows * d * f / t / 1e12, 4), "unit": "TOPS",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle w8a8_mlp on {sample_rows} of {inp['x'].shape[0]} tokens, full {d}->{f}->{d} "
+                      f"weights, median of {repeats} runs ({t:.2f} s each), torch {torch.__version__}"}
+
+
+def cpu_baseline_norm_rope(nr: dict, repeats: int = 3) -> dict:
+    import torch
+
+    from oracle import cpu_ref
+
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        for x in (nr["q"], nr["k"]):
+            cpu_ref.norm_rope(x, nr["scale"], nr["shift"], nr["freqs"], nr["head_dim"], nr["eps"])
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    m, d = nr["q"].shape
+    return {"value": round(8.0 * m * d / t / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"oracle norm_rope on Q and K, full {m}x{d}, median of {repeats}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-rows", type=int, default=2048)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the path shards along "
+              f"tokens with no exchange; run one process per GPU)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    from x_minimaxh3_amd import _lib, workloads
+
+    pkg.ensure_library()
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device: {props.name} CUs={props.multi_processor_count}")
+
+    # ------------------------------------------------------------------ MLP
+    cfg = workloads.CONFIGS["mlp_720p"]
+    M, D, F = cfg["M"], cfg["d"], cfg["ffn"]
+    log(f"generating W8A8 MLP inputs M={M} d={D} ffn={F}")
+    inp = workloads.mlp_inputs(**cfg, seed=0)
+    x, w1, s1, w2, s2 = (inp[k].to(dev) for k in ("x", "w1", "s1", "w2", "s2"))
+    st = _lib.stream_of(x)
+    q1 = torch.empty(M, D, dtype=torch.int8, device=dev)
+    sx = torch.empty(M, dtype=torch.float32, device=dev)
+    g = torch.empty(M, F, dtype=torch.bfloat16, device=dev)
+    amax = torch.empty(M, dtype=torch.int32, device=dev)
+    q2 = torch.empty(M, F, dtype=torch.int8, device=dev)
+    sg = torch.empty(M, dtype=torch.float32, device=dev)
+    y = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+
+    def step(ev):
+        if ev:
+            ev[0].record()
+        _lib.call("xmh3_quantize_int8_rowwise_ex", x.data_ptr(), 2, 0, M, D, D, q1.data_ptr(), sx.data_ptr(),
+                  amax.data_ptr(), st)
+        if ev:
+            ev[1].record()
+        _lib.call("xmh3_int8_gemm", q1.data_ptr(), D, w1.data_ptr(), D, M, F, D, sx.data_ptr(), s1.data_ptr(), 1,
+                  None, g.data_ptr(), 2, F, 1, amax.data_ptr(), st)
+        if ev:
+            ev[2].record()
+        _lib.call("xmh3_requant_int8_rows", g.data_ptr(), 2, M, F, F, amax.data_ptr(), q2.data_ptr(),
+                  sg.data_ptr(), st)
+        if ev:
+            ev[3].record()
+        _lib.call("xmh3_int8_gemm", q2.data_ptr(), F, w2.data_ptr(), F, M, D, F, sg.data_ptr(), s2.data_ptr(), 1,
+                  None, y.data_ptr(), 2, D, 0, None, st)
+        if ev:
+            ev[4].record()
+
+    for _ in range(args.warmup):
+        step(None)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    names = ("quant", "fc1_gemm_gelu", "requant", "fc2_gemm")
+    kavg = {n: statistics.mean(ev[j].elapsed_time(ev[j + 1]) for ev in evs) for j, n in enumerate(names)}
+    ms_step = wall * 1e3 / args.steps
+    ops = 4.0 * M * D * F
+    tops = ops / (ms_step * 1e-3) / 1e12
+    gemm_ops = 2.0 * M * D * F
+    fc1_tops = gemm_ops / (kavg["fc1_gemm_gelu"] * 1e-3) / 1e12
+    fc2_tops = gemm_ops / (kavg["fc2_gemm"] * 1e-3) / 1e12
+    log(f"mlp: {ms_step:.3f} ms/step wall ({tops:.1f} TOPS), kernel sum {sum(kavg.values()):.3f} ms: "
+        + ", ".join(f"{k}={v:.3f}" for k, v in kavg.items()))
+
+    # ------------------------------------------------------------------ norm-rope
+    nr = workloads.norm_rope_inputs(grid=workloads.CONFIGS["norm_rope_720p"]["grid"])
+    qd, kd = nr["q"].to(dev), nr["k"].to(dev)
+    scd, shd, fd = nr["scale"].to(dev), nr["shift"].to(dev), nr["freqs"].to(dev)
+    Mn, Dn = qd.shape
+    qo, ko = torch.empty_like(qd), torch.empty_like(kd)
+    ft = fd.reshape(Mn, -1)
+
+    def nr_step():
+        _lib.call("xmh3_norm_rope", qd.data_ptr(), qo.data_ptr(), kd.data_ptr(), ko.data_ptr(), 2, Mn, Dn, Dn, Dn,
+                  scd.data_ptr(), shd.data_ptr(), 2, Dn, Mn, ft.data_ptr(), 0, ft.stride(0), 128, 1e-6, st)
+
+    for _ in range(args.warmup):
+        nr_step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        nr_step()
+    e1.record()
+    torch.cuda.synchronize()
+    nr_ms = e0.elapsed_time(e1) / args.steps
+    nr_bytes = 8.0 * Mn * Dn
+    nr_gbs = nr_bytes / (nr_ms * 1e-3) / 1e9
+    log(f"norm_rope: {nr_ms * 1e3:.1f} us/launch, {nr_gbs:.0f} GB/s ({nr_gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
+
+    # ------------------------------------------------------------------ CPU baseline
+    cpu = None
+    cpu_nr = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle) ...")
+        cpu = cpu_baseline_mlp(inp, args.cpu_sample_rows)
+        cpu_nr = cpu_baseline_norm_rope(nr)
+        log(f"cpu: mlp {cpu['value']} TOPS, norm_rope {cpu_nr['value']} GB/s")
+
+    out = {
+        "metric": "W8A8 MLP INT8 TOPS (%peak) + norm-rope HBM GB/s at M=25200, d=5120, 1 GPU",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded N(0,1) activations with 1% x20 outlier channels, N(0,0.02) weights "
+                "quantised per channel)",
+        "config": {"workload": "w8a8_mlp_720p", "tokens": M, "d_model": D, "ffn": F,
+                   "mlp": "fc2(gelu_tanh(fc1(x))), per-token int8 activations, per-channel int8 weights",
+                   "norm_rope_workload": "norm_rope_720p", "grid": [7, 45, 80], "heads": 40, "head_dim": 128},
+        "frac_of_peak": round(tops / PEAK_INT8_TOPS, 4),
+        "kernels_ms": {k: round(v, 4) for k, v in kavg.items()},
+        "roofline": {"kernel": "gemm_i8_kernel (fc1, dequant+GELU+row-amax epilogue)", "bound": "mfma",
+                     "achieved": round(fc1_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                     "frac": round(fc1_tops / PEAK_INT8_TOPS, 4), "traffic": None,
+                     "algorithmic": "2*M*d*ffn int8 ops per launch"},
+        "roofline_fc2": {"kernel": "gemm_i8_kernel (fc2, dequant epilogue)", "bound": "mfma",
+                         "achieved": round(fc2_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
+                         "frac": round(fc2_tops / PEAK_INT8_TOPS, 4), "traffic": None},
+        "norm_rope": {"kernel": "rowspan_kernel (Q and K)", "bound": "hbm", "achieved": round(nr_gbs, 1),
+                      "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(nr_gbs / PEAK_HBM_GBS, 4),
+                      "us_per_launch": round(nr_ms * 1e3, 2), "traffic": None,
+                      "algorithmic": "8*M*d bytes (Q,K read + written, bf16)"},
+        "cpu_baseline": cpu,
+        "cpu_baseline_norm_rope": cpu_nr,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,180 @@
+/*
+ * xmh3.h -- C ABI of the MI355X (gfx950) quantized DiT-block hot path.
+ *
+ * Library: x-minimaxh3_amd/libxmh3_hip.so (hipcc, gfx950 only).
+ *
+ * Conventions
+ *   - Plain pointers to device memory, int64 sizes/strides (in elements unless
+ *     stated), int dtype codes, and the caller's HIP stream. Nothing here
+ *     allocates; outputs and workspaces are owned by the caller.
+ *   - dtype codes follow the reference's op boundary
+ *     (CK/backends/eager/quantization.py:34-42): 0 fp32, 1 fp16, 2 bf16.
+ *   - input-activation codes follow CK/backends/_activations.py:19-24:
+ *     0 none, 1 gelu_tanh (2 swiglu is not implemented here).
+ *   - Every entry point returns 0 on success, 1 invalid argument, 2 HIP
+ *     launch error, 3 unsupported combination; the message is available from
+ *     xmh3_last_error() on the calling thread. No C++ exception crosses the
+ *     ABI. All work is stream-ordered; no entry point synchronises the host.
+ *
+ * Reference paths are relative to the reference root; CK abbreviates
+ * backends/turbo/vendor/comfy_kitchen.
+ */
+#ifndef XMH3_H
+#define XMH3_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* xmh3_stream_t; /* == hipStream_t */
+
+/* Message of the last failing call on this thread. */
+const char* xmh3_last_error(void);
+int xmh3_abi_version(void);
+
+/*
+ * Per-token dynamic int8 quantisation, optionally after GELU-tanh.
+ * Replaces: CK/backends/cuda/ops/int8_linear.cu:1035
+ *   launch_quantize_int8_rowwise_kernel(in, out, scales, M, K, dtype, ...)
+ * (semantics of CK/backends/eager/quantization.py:857-875, the public op
+ * CK/__init__.py:702-709 quantize_int8_rowwise; the activation of
+ * CK/backends/_activations.py:40-53).
+ * x: [M, ldx] of x_dtype; q: int8 [M, K] contiguous; scale: fp32 [M].
+ */
+int xmh3_quantize_int8_rowwise(const void* x, int x_dtype, int input_act, int64_t M, int64_t K,
+                               int64_t ldx, int8_t* q, float* scale, xmh3_stream_t stream);
+
+/*
+ * As xmh3_quantize_int8_rowwise, and also writes 0 to clear_rows[0..M) (the
+ * row-|max| slots the fused MLP's fc1 epilogue accumulates into; NULL = none):
+ * the first kernel of the MLP chain. Same reference interface as above.
+ */
+int xmh3_quantize_int8_rowwise_ex(const void* x, int x_dtype, int input_act, int64_t M, int64_t K,
+                                  int64_t ldx, int8_t* q, float* scale, uint32_t* clear_rows,
+                                  xmh3_stream_t stream);
+
+/*
+ * Requantise rows whose |max| is already known (bit pattern of the fp32
+ * value), the second half of the fused MLP's per-token requant.
+ * Replaces the quantizer call inside the fc2 int8_linear with
+ * input_act="gelu_tanh" (CK/backends/eager/quantization.py:998,1023).
+ * g: bf16/fp16 [M, ldg]; q: int8 [M, K]; scale: fp32 [M].
+ */
+int xmh3_requant_int8_rows(const void* g, int g_dtype, int64_t M, int64_t K, int64_t ldg,
+                           const uint32_t* row_absmax_bits, int8_t* q, float* scale,
+                           xmh3_stream_t stream);
+
+/*
+ * int8 x int8 -> int32 GEMM on MFMA with a fused epilogue:
+ *   epilogue 0: out = T(float(acc) * (sx[m] * sw[n])) (+ bias[n] in T)
+ *   epilogue 1: as 0 in bf16, then g = bf16(gelu_tanh(.)) stored, and max|g|
+ *               per row folded into row_absmax_bits (must start at 0)
+ *   epilogue 2: raw int32 accumulators into out (int32 [M, ldo])
+ * A: int8 [M, lda] (activations), B: int8 [N, ldb] (weights, row = output
+ * channel), K % 16 == 0, lda/ldb multiples of 16 bytes.
+ * Replaces: CK/backends/cuda/ops/cutlass_gemm_int8.cu:612-683
+ *   bool launch_cutlass_int8_dequant(a, b, xs, ws, bias, d, M, N, K, out_code, stream)
+ * and the dequant kernel CK/backends/cuda/ops/int8_linear.cu:343-409
+ * (eager order CK/backends/eager/quantization.py:1028-1054).
+ */
+int xmh3_int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_t M,
+                   int64_t N, int64_t K, const float* sx, const float* sw, int sw_per_channel,
+                   const void* bias, void* out, int out_dtype, int64_t ldo, int epilogue,
+                   uint32_t* row_absmax_bits, xmh3_stream_t stream);
+
+/*
+ * Grouped int4 -> int8 grid decode (low nibble = even k).
+ * Replaces: CK/backends/cuda/ops/w4a8_gemm.cu:94
+ *   launch_dequant_int4_grouped_to_int8(qw, s_rel, codebook, out, N, K, G, stream)
+ * (eager CK/backends/eager/w4a8_int8.py:344-363).
+ * packed: uint8 [N, K/2]; s_rel: fp32 or bf16 [N, K/G]; codebook: fp32 [16]
+ * or NULL (levels code-8); out: int8 [N, K].
+ */
+int xmh3_w4_decode_int8(const uint8_t* packed, const void* s_rel, int s_rel_dtype,
+                        const float* codebook, int64_t N, int64_t K, int64_t group_size,
+                        int8_t* out, xmh3_stream_t stream);
+
+/*
+ * The W8A8 MLP block y = fc2(gelu_tanh(fc1(x))), bf16 output.
+ * Replaces the MLP driver's two int8_linear calls
+ * (h3serve/native_engine/model/fused_mlp.py:343-405, the op chain
+ * CK/__init__.py:722-764 with input_act="gelu_tanh" on fc2).
+ * x: [M, ldx] of x_dtype; w1: int8 [F, D]; s1: fp32 [F] or [1];
+ * w2: int8 [D, F]; s2: fp32 [D] or [1]; y: bf16 [M, ldy].
+ * workspace: xmh3_w8a8_mlp_workspace_bytes(M, D, F) bytes of device memory.
+ */
+size_t xmh3_w8a8_mlp_workspace_bytes(int64_t M, int64_t D, int64_t F);
+int xmh3_w8a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                  const int8_t* w1, const float* s1, int s1_per_channel, const int8_t* w2,
+                  const float* s2, int s2_per_channel, void* y, int64_t ldy, void* workspace,
+                  size_t workspace_bytes, xmh3_stream_t stream);
+
+/*
+ * The W4A8 MLP block: grouped int4 weights (uniform levels, no rotation),
+ * s_rel fp32 or bf16 [N, K/G], per-channel fp32 s_channel.
+ * Replaces: the chunked W4A8 MLP (h3serve/native_engine/model/fused_mlp.py:222-266)
+ * over w4a8_int8_linear (CK/tensor/w4a8_int8.py:89-115, eager
+ * CK/backends/eager/w4a8_int8.py:457-508 decomposed as decode + int8_linear).
+ */
+size_t xmh3_w4a8_mlp_workspace_bytes(int64_t M, int64_t D, int64_t F);
+int xmh3_w4a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                  const uint8_t* w1_packed, const void* w1_srel, const float* w1_schannel,
+                  const uint8_t* w2_packed, const void* w2_srel, const float* w2_schannel,
+                  int srel_dtype, int64_t group_size, void* y, int64_t ldy, void* workspace,
+                  size_t workspace_bytes, xmh3_stream_t stream);
+
+/*
+ * Fused AdaLN-modulated RMSNorm + split-half RoPE for Q and K of the same
+ * tokens (k_in/k_out may be NULL): RMS over the full row of `width`, rotation
+ * per head of head_dim (64, 128 or 256) with a table [tokens or 1,
+ * head_dim/2, 2, 2] of freqs_dtype (fp32 or x's dtype); scale/shift rows
+ * [R, mod_ld] of x's dtype, token t uses row t / mod_group (NULL: no AdaLN).
+ * In-place is allowed (q_out == q_in).
+ * Replaces: rms_adaln (CK/__init__.py:130-150, eager CK/backends/eager/adaln.py:17-20)
+ * followed by apply_rope_split_half (CK/__init__.py:629-650, eager
+ * CK/backends/eager/rope.py:39-48).
+ */
+int xmh3_norm_rope(const void* q_in, void* q_out, const void* k_in, void* k_out, int dtype,
+                   int64_t tokens, int64_t width, int64_t ld_in, int64_t ld_out, const void* scale,
+                   const void* shift, int mod_dtype, int64_t mod_ld, int64_t mod_group,
+                   const void* freqs, int freqs_dtype, int64_t freqs_token_stride, int head_dim,
+                   float eps, xmh3_stream_t stream);
+
+/*
+ * rms_norm(x [* norm_weight]) * (1 + scale[r]) + shift[r], r = row_map[t]
+ * (if non-NULL) else t / mod_group; output in torch's promoted dtype of
+ * (x, scale).
+ * Replaces: CK/backends/cuda/ops/adaln.cu:256-313 (launcher of the
+ * (RMS-)AdaLN kernels), eager CK/backends/eager/adaln.py:17-20; with
+ * norm_weight and row_map the H3 segmented form
+ * h3serve/native_engine/model/kernels.py:7586-7634.
+ */
+int xmh3_rms_adaln(const void* x, void* out, int dtype, int64_t rows, int64_t width, int64_t ld_in,
+                   int64_t ld_out, const void* norm_weight, const void* scale, const void* shift,
+                   int mod_dtype, int64_t mod_ld, const int32_t* row_map, int64_t mod_group,
+                   float eps, xmh3_stream_t stream);
+
+/*
+ * Split-half RoPE on strided [B, S, H, head_dim] (last dim contiguous), with
+ * (norm=1) or without (norm=0) the per-head RMSNorm with weight; rotates the
+ * first rot_dim dims (0 = all), the tail is norm-only. out may alias x.
+ * freqs: [*, *, *, rot_dim/2, 2, 2] with element strides freqs_strides[0..2]
+ * over (B, S, H) (0 = broadcast).
+ * Replaces: CK/backends/cuda/ops/rms_rope.cu:353-384
+ *   launch_rms_rope_kernel(...) (split-half mode), eager
+ *   CK/backends/eager/rope.py:67-92,178-189 and 39-48.
+ */
+int xmh3_rope_split_half(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H,
+                         int64_t head_dim, const int64_t* x_strides, const int64_t* out_strides,
+                         const void* norm_weight, int weight_dtype, const void* freqs,
+                         int freqs_dtype, const int64_t* freqs_strides, int rot_dim, float eps,
+                         int norm, xmh3_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XMH3_H */

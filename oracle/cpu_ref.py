@@ -1,0 +1,344 @@
+"""torch-CPU restatement of the reference's eager path (the oracle).
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``): imported by tests,
+by ``__graft_entry__.smoke()`` as the checker and by ``bench.py``'s
+``cpu_baseline`` leg. The product path never imports it.
+
+Citations are relative to the reference root; ``CK/`` abbreviates the
+vendored kernel library ``backends/turbo/vendor/comfy_kitchen/``.
+
+Every function follows the reference's op order exactly and calls the same
+torch CPU routines the reference calls (``torch._int_mm``, ``F.gelu``,
+``F.rms_norm``), so the rounding points (each bf16 materialisation) are the
+reference's own.
+
+Pinning (what checks each function independently of this file; the tests
+live in ``tests/test_oracle.py``):
+
+* ``quantize_int8_rowwise``  -- numpy restatement (``npref``), the C
+  restatement (``c/oracle.c``) and hand-built special cases (zero row,
+  -127.5 -> -128, +127.5 -> 127, half-to-even ties).
+* ``int8_mm``                -- int64 brute force (numpy and C).
+* ``dequant``/``int8_linear``-- float64 closed form + the C restatement of
+  the fp32 epilogue; composite order vs a step-by-step numpy restatement.
+* ``gelu_tanh``              -- the library routine itself (``F.gelu``),
+  checked against the float64 closed form within 1 bf16 ulp.
+* ``quantize_w4_weight`` / ``dequant_int4_grouped_to_int8`` -- numpy
+  restatement, pure-Python loops on tiny inputs, nibble-order and
+  round-trip invariants.
+* ``rms_adaln`` / ``rms_norm`` -- float64 closed form within 1 bf16 ulp and
+  the special case scale=shift=0 reducing to ``F.rms_norm``.
+* ``rope_table``             -- closed form (cos/sin of integer position
+  times theta^(-2i/dim)) and the unit-modulus invariant.
+* ``apply_rope_split_half1`` -- complex-multiplication form, identity table
+  reduces to the input, norm-preservation invariant.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+
+DTYPE_CODE_TO_DTYPE = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}
+
+
+# ---------------------------------------------------------------------------
+# a1: per-token dynamic int8 quantisation
+# ---------------------------------------------------------------------------
+
+def _int8_scale_for_math(scale: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """CK/backends/eager/quantization.py:815-818: the scale in x's dtype,
+    zeros replaced by that dtype's smallest normal."""
+    scale = scale.to(dtype=x.dtype)
+    tiny = torch.finfo(x.dtype).tiny
+    return torch.where(scale == 0, torch.full_like(scale, tiny), scale)
+
+
+def quantize_int8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """CK/backends/eager/quantization.py:857-875 (with _round_int8 :821-826,
+    stochastic_rounding=0).
+
+    amax in x's dtype; scale = max(amax.float()/127, 1e-30) (fp32, true
+    division); v = x / scale.to(x.dtype) in x's dtype; round half to even;
+    clamp [-128, 127]. Returns (int8 [...,K], fp32 [...,1]) with the
+    unrounded fp32 scale.
+    """
+    abs_max = x.abs().amax(dim=-1, keepdim=True)
+    scale = (abs_max.float() / 127.0).clamp(min=1e-30)
+    scaled = x / _int8_scale_for_math(scale, x)
+    q = scaled.round_().clamp_(-128.0, 127.0).to(torch.int8)
+    return q, scale
+
+
+# ---------------------------------------------------------------------------
+# a2: input activation
+# ---------------------------------------------------------------------------
+
+def apply_input_act(x: torch.Tensor, input_act: str | None) -> torch.Tensor:
+    """CK/backends/_activations.py:40-53."""
+    if input_act in (None, "none"):
+        return x
+    if input_act == "gelu_tanh":
+        return F.gelu(x, approximate="tanh")
+    if input_act == "swiglu":
+        gate, up = x.chunk(2, dim=-1)
+        return F.silu(gate).mul_(up)
+    raise ValueError(f"unsupported input_act: {input_act!r}")
+
+
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    return apply_input_act(x, "gelu_tanh")
+
+
+# ---------------------------------------------------------------------------
+# a3/a4: int8 GEMM and the dequant epilogue
+# ---------------------------------------------------------------------------
+
+def int8_mm(a: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """CK/backends/eager/quantization.py:749-783 on CPU: int32 accumulators of
+    a[M,K] @ w[N,K]^T. On CPU the reference pads K to a multiple of 8 and N to
+    a multiple of 8 with zeros (no effect on the sums) and calls torch._int_mm."""
+    m, k = a.shape
+    n = w.shape[0]
+    b = w.t().contiguous()
+    if m == 0 or k == 0:
+        return torch.zeros(m, n, dtype=torch.int32)
+    pk = (k + 7) // 8 * 8
+    if pk != k:
+        a = torch.cat((a, torch.zeros(m, pk - k, dtype=a.dtype)), dim=1)
+        b = torch.cat((b, torch.zeros(pk - k, n, dtype=b.dtype)), dim=0)
+    pn = (n + 7) // 8 * 8
+    if pn != n:
+        b = torch.cat((b, torch.zeros(b.shape[0], pn - n, dtype=b.dtype)), dim=1)
+    return torch._int_mm(a, b)[:, :n]
+
+
+def dequant(acc: torch.Tensor, x_scale: torch.Tensor, w_scale: torch.Tensor,
+            out_dtype: torch.dtype = torch.bfloat16,
+            bias: torch.Tensor | None = None) -> torch.Tensor:
+    """CK/backends/eager/quantization.py:1028-1054: out = (acc.float() *
+    (x_scale * w_scale)).to(out_dtype), the scale product formed first in
+    fp32, then bias added in out_dtype."""
+    ws = w_scale.to(torch.float32).reshape(1, -1)
+    out = (acc.float() * (x_scale.to(torch.float32).reshape(-1, 1) * ws)).to(out_dtype)
+    if bias is not None:
+        out = out + bias.to(dtype=out.dtype).reshape(1, -1)
+    return out
+
+
+def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                bias: torch.Tensor | None = None,
+                out_dtype: torch.dtype = torch.bfloat16,
+                input_act: str | None = None,
+                return_parts: bool = False):
+    """CK/backends/eager/quantization.py:971-1056 with convrot=False:
+    act -> rowwise quant -> int8 GEMM -> fp32 dequant -> cast -> bias."""
+    x = apply_input_act(x, input_act)
+    if x.shape[-1] != weight.shape[-1]:
+        raise ValueError("Input and weight inner dimensions must match")
+    ws = weight_scale.to(torch.float32).reshape(-1)
+    if ws.numel() not in (1, weight.shape[0]):
+        raise ValueError("INT8 weight scale must be scalar or per-output-channel")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, x.shape[-1])
+    q, s = quantize_int8_rowwise(x2)
+    acc = int8_mm(q, weight)
+    out = dequant(acc, s, ws, out_dtype, bias).reshape(*lead, weight.shape[0])
+    if return_parts:
+        return out, {"act": x2, "q": q, "scale": s, "acc": acc}
+    return out
+
+
+# ---------------------------------------------------------------------------
+# a5/a6: the W8A8 MLP block  y = fc2(gelu_tanh(fc1(x)))
+# ---------------------------------------------------------------------------
+
+def w8a8_mlp(x: torch.Tensor, w1: torch.Tensor, s1: torch.Tensor,
+             w2: torch.Tensor, s2: torch.Tensor, return_parts: bool = False):
+    """fc1 = int8_linear(x, W1, s1); fc2 = int8_linear(fc1, W2, s2,
+    input_act="gelu_tanh") -- the reference op API form of the GELU-tanh MLP
+    (CK/__init__.py:722-764; the H3 driver's fc2 call with a fused input act,
+    h3serve/native_engine/model/fused_mlp.py:396-405)."""
+    h, p1 = int8_linear(x, w1, s1, return_parts=True)
+    y, p2 = int8_linear(h, w2, s2, input_act="gelu_tanh", return_parts=True)
+    if return_parts:
+        return y, {"q1": p1["q"], "s1": p1["scale"], "acc1": p1["acc"], "h": h,
+                   "g": p2["act"], "q2": p2["q"], "s2": p2["scale"], "acc2": p2["acc"]}
+    return y
+
+
+# ---------------------------------------------------------------------------
+# a7/a8: W4A8 (int4 grouped, uniform levels, no rotation)
+# ---------------------------------------------------------------------------
+
+def quantize_w4_weight(weight: torch.Tensor, group_size: int = 128):
+    """CK/backends/eager/w4a8_int8.py:122-209, branch symmetric=True,
+    codebook=False, scale_dtype=float32 (:169-173, :188-191):
+
+    gs = max(amax_g/7, 1e-8); signed = clamp(round(w/gs), -8, 7);
+    u = signed + 8; s_channel = max(amax_n(|signed*gs|)/127, 1e-8);
+    s_rel = gs / s_channel; byte = (u[2j] & 0xF) | (u[2j+1] << 4).
+    Returns (packed int8 [N,K/2], s_rel fp32 [N,K/G], s_channel fp32 [N]).
+    """
+    n, k = weight.shape
+    groups = k // group_size
+    gw = weight.float().view(n, groups, group_size)
+    group_scale = (gw.abs().amax(dim=-1, keepdim=True) / 7.0).clamp(min=1e-8)
+    signed = (gw / group_scale).round().clamp(-8, 7).to(torch.int32)
+    unsigned = (signed + 8).view(n, k)
+    shifted = signed * group_scale
+    s_channel = (shifted.abs().amax(dim=(1, 2)) / 127.0).clamp(min=1e-8)
+    s_rel = (group_scale.squeeze(-1) / s_channel.unsqueeze(1)).float().contiguous()
+    packed = ((unsigned[:, 0::2] & 0xF) | ((unsigned[:, 1::2] & 0xF) << 4)).to(torch.int8).contiguous()
+    return packed, s_rel, s_channel.float().contiguous()
+
+
+def dequant_int4_grouped_to_int8(qdata: torch.Tensor, s_rel: torch.Tensor,
+                                 group_size: int, codebook: torch.Tensor | None = None) -> torch.Tensor:
+    """CK/backends/eager/w4a8_int8.py:344-363: code[2j] = b & 0xF,
+    code[2j+1] = (b >> 4) & 0xF; level = code - 8 (or codebook[code]);
+    int8 = clamp(round(level * s_rel.float()), -127, 127)."""
+    n, k_half = qdata.shape
+    k = k_half * 2
+    groups = k // group_size
+    packed = qdata.to(torch.int32) & 0xFF
+    quantized = torch.empty(n, k, dtype=torch.int32)
+    quantized[:, 0::2] = packed & 0xF
+    quantized[:, 1::2] = (packed >> 4) & 0xF
+    if codebook is not None:
+        values = codebook.to(torch.float32)[quantized]
+    else:
+        values = quantized.float() - 8.0
+    values = values.view(n, groups, group_size) * s_rel.float().unsqueeze(-1)
+    return values.view(n, k).round().clamp_(-127, 127).to(torch.int8)
+
+
+def w4a8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor,
+                s_channel: torch.Tensor, group_size: int = 128,
+                bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                input_act: str | None = None) -> torch.Tensor:
+    """CK/backends/eager/w4a8_int8.py:457-508 without the forced ConvRot:
+    decode to the int8 grid, then int8_linear with s_channel as the
+    per-channel weight scale."""
+    w8 = dequant_int4_grouped_to_int8(qdata, s_rel, group_size)
+    return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype, input_act=input_act)
+
+
+def w4a8_mlp(x, w1_packed, w1_srel, w1_sch, w2_packed, w2_srel, w2_sch, group_size=128):
+    h = w4a8_linear(x, w1_packed, w1_srel, w1_sch, group_size)
+    return w4a8_linear(h, w2_packed, w2_srel, w2_sch, group_size, input_act="gelu_tanh")
+
+
+# ---------------------------------------------------------------------------
+# a9: (segmented) AdaLN-modulated RMSNorm
+# ---------------------------------------------------------------------------
+
+def rms_adaln(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+              eps: float = 1e-6) -> torch.Tensor:
+    """CK/backends/eager/adaln.py:17-20:
+    F.rms_norm(x, (D,), eps) * (1 + scale) + shift, every op in torch's
+    promoted dtype (bf16 x and bf16 scale/shift round after each op)."""
+    normalized = F.rms_norm(x, x.shape[-1:], eps=eps)
+    return normalized * (1 + scale) + shift
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """h3serve/native_engine/model/layers.py:39-48 (RMSNorm.forward)."""
+    w = None if weight is None else weight.to(dtype=x.dtype)
+    return F.rms_norm(x, (x.shape[-1],), weight=w, eps=eps)
+
+
+def rms_adaln_segmented(value: torch.Tensor, norm_weight: torch.Tensor | None,
+                        shift: torch.Tensor, scale: torch.Tensor,
+                        segments, eps: float = 1e-5) -> torch.Tensor:
+    """h3serve/native_engine/model/kernels.py:7623-7634 (the eager order of
+    rms_adaln with segments): hidden = RMSNorm(value); per segment
+    hidden.mul_(1 + scale[row]).add_(shift[row])."""
+    hidden = rms_norm(value, norm_weight, eps)
+    previous = 0
+    for start, stop, row in segments:
+        if start != previous or stop <= start:
+            raise ValueError("modulation segments must be an ordered partition")
+        hidden[start:stop].mul_(1.0 + scale[row].to(hidden.dtype)).add_(shift[row].to(hidden.dtype))
+        previous = stop
+    if previous != hidden.shape[0]:
+        raise ValueError("modulation segments do not cover the packed sequence")
+    return hidden
+
+
+# ---------------------------------------------------------------------------
+# a10: RoPE table for a T x H x W token grid
+# ---------------------------------------------------------------------------
+
+def grid_positions(t: int, h: int, w: int) -> torch.Tensor:
+    """t-major integer positions [(t,h,w)] (h3serve/native_engine/model/packed.py:343)."""
+    tt, hh, ww = torch.meshgrid(torch.arange(t), torch.arange(h), torch.arange(w), indexing="ij")
+    return torch.stack((tt.reshape(-1), hh.reshape(-1), ww.reshape(-1)), dim=-1)
+
+
+def axis_inv_freq(dims=(44, 42, 42), theta: float = 10000.0) -> list[torch.Tensor]:
+    """theta^(-2i/dim) for i < dim/2, per axis: evaluated in float64, then
+    rounded once to fp32."""
+    return [(1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d))).float() for d in dims]
+
+
+def rope_table(positions: torch.Tensor, dims=(44, 42, 42), theta: float = 10000.0,
+               dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """h3serve/native_engine/model/layers.py:51-69: per-axis angles pos*inv_freq
+    concatenated [t|h|w]; table = stack(cos, -sin, sin, cos) as
+    [1, S, 1, half, 2, 2] in ``dtype``."""
+    inv = axis_inv_freq(dims, theta)
+    per_axis = [positions[:, a:a + 1].float() * inv[a].reshape(1, -1) for a in range(3)]
+    angles = torch.cat(per_axis, dim=-1)              # [S, half]
+    cosine, sine = torch.cos(angles), torch.sin(angles)
+    half = angles.shape[-1]
+    return torch.stack((cosine, -sine, sine, cosine), dim=-1).reshape(
+        1, angles.shape[0], 1, half, 2, 2).to(dtype)
+
+
+# ---------------------------------------------------------------------------
+# a11/a12: split-half RoPE, with or without the per-head RMSNorm
+# ---------------------------------------------------------------------------
+
+def apply_rope_split_half1(x: torch.Tensor, freqs_cis: torch.Tensor) -> torch.Tensor:
+    """CK/backends/eager/rope.py:39-42: rotate pairs (i, i+D/2) in the table's
+    dtype: out0 = f00*x0 + f01*x1, out1 = f10*x0 + f11*x1, then cast back."""
+    t_ = x.reshape(*x.shape[:-1], 2, -1).movedim(-2, -1).unsqueeze(-2).to(freqs_cis.dtype)
+    t_out = freqs_cis[..., 0] * t_[..., 0] + freqs_cis[..., 1] * t_[..., 1]
+    return t_out.movedim(-1, -2).reshape(*x.shape).type_as(x)
+
+
+def rms_rope_split_half1(x: torch.Tensor, freqs_cis: torch.Tensor, weight: torch.Tensor,
+                         eps: float = 1e-6, rot_dim: int = 0) -> torch.Tensor:
+    """CK/backends/eager/rope.py:67-92 (split_half=True): per-head
+    F.rms_norm with weight, rotate the first rot_dim dims, tail norm-only."""
+    x_norm = F.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
+    if rot_dim and rot_dim != x.shape[-1]:
+        rotated = apply_rope_split_half1(x_norm[..., :rot_dim], freqs_cis)
+        return torch.cat((rotated, x_norm[..., rot_dim:]), dim=-1)
+    return apply_rope_split_half1(x_norm, freqs_cis)
+
+
+def norm_rope(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+              freqs_cis: torch.Tensor, head_dim: int = 128, eps: float = 1e-6) -> torch.Tensor:
+    """The fused AdaLN-RMSNorm + 3D RoPE composite for one of Q or K:
+    apply_rope_split_half(rms_adaln(x, scale, shift, eps), freqs) with the
+    RMS over the full row and the rotation per head
+    (CK/backends/eager/adaln.py:17-20 then CK/backends/eager/rope.py:39-42).
+    x: [M, D] with D = heads*head_dim; freqs: [1, M, 1, head_dim/2, 2, 2]."""
+    m, d = x.shape
+    a = rms_adaln(x, scale, shift, eps)
+    a4 = a.reshape(1, m, d // head_dim, head_dim)
+    return apply_rope_split_half1(a4, freqs_cis).reshape(m, d)
+
+
+def bf16_ulp_diff(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """|a-b| in units of bf16 ulp at b's magnitude (helper for tolerances)."""
+    bf = b.float().abs().clamp(min=2.0 ** -126)
+    ulp = torch.pow(2.0, torch.floor(torch.log2(bf)) - 7)
+    return (a.float() - b.float()).abs() / ulp
+
+
+__all__ = [name for name in dir() if not name.startswith("_") and name not in ("math", "torch", "F")]

@@ -1,0 +1,70 @@
+"""The C-ABI library loads and exports every symbol include/xmh3.h declares
+(no compute calls: runs without a GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "xmh3.h"
+LIB = ROOT / "x-minimaxh3_amd" / "libxmh3_hip.so"
+
+
+def declared_symbols() -> set[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(xmh3_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("xmh3_quantize_int8_rowwise", "xmh3_int8_gemm", "xmh3_w8a8_mlp", "xmh3_w4a8_mlp",
+              "xmh3_norm_rope", "xmh3_rms_adaln", "xmh3_rope_split_half", "xmh3_w4_decode_int8",
+              "xmh3_last_error"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(LIB))
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    lib.xmh3_abi_version.restype = ctypes.c_int
+    assert lib.xmh3_abi_version() == 1
+
+
+def test_binding_table_matches_header(pkg):
+    from x_minimaxh3_amd import _lib
+
+    assert set(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_workspace_queries_without_gpu(pkg):
+    from x_minimaxh3_amd import _lib
+
+    lib = _lib.load()
+    n = lib.xmh3_w8a8_mlp_workspace_bytes(25200, 5120, 13824)
+    # q1 + sx + g(bf16) + amax + q2 + sg, each 256-byte aligned
+    expect = 0
+    for b in (25200 * 5120, 25200 * 4, 25200 * 13824 * 2, 25200 * 4, 25200 * 13824, 25200 * 4):
+        expect += (b + 255) // 256 * 256
+    assert n == expect
+    assert lib.xmh3_w4a8_mlp_workspace_bytes(64, 256, 512) > lib.xmh3_w8a8_mlp_workspace_bytes(64, 256, 512)
+
+
+def test_argument_errors_need_no_gpu(pkg):
+    """Shape validation happens before any launch: bad arguments return status 1
+    with a message, and nothing crosses the ABI as an exception."""
+    from x_minimaxh3_amd import _lib
+
+    lib = _lib.load()
+    rc = lib.xmh3_int8_gemm(None, 16, None, 16, 4, 4, 17, None, None, 0, None, None, 2, 4, 0, None, None)
+    assert rc == 1
+    assert b"K must be a multiple of 16" in lib.xmh3_last_error() or b"null" in lib.xmh3_last_error()
+    rc = lib.xmh3_quantize_int8_rowwise(None, 2, 2, 4, 16, 16, None, None, None)
+    assert rc == 1 and b"input_act" in lib.xmh3_last_error()
+    rc = lib.xmh3_w8a8_mlp(None, 2, 8, 100, 64, 100, None, None, 1, None, None, 1, None, 100, None, 0, None)
+    assert rc == 1 and b"multiples of 16" in lib.xmh3_last_error()

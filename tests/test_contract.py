@@ -1,0 +1,126 @@
+"""Host-side contract of the op boundary (CPU only): dispatch errors, argument
+validation with the reference's error types, in-place guards, modulation
+broadcast grouping and the workload generators."""
+
+import pytest
+import torch
+
+from oracle import cpu_ref
+
+
+def test_cpu_tensors_fail_loudly(pkg):
+    x = torch.randn(4, 64).bfloat16()
+    with pytest.raises(pkg.NoCapableBackendError, match="device cpu"):
+        pkg.int8_linear(x, torch.zeros(8, 64, dtype=torch.int8), torch.ones(8))
+    with pytest.raises(pkg.NoCapableBackendError):
+        pkg.quantize_int8_rowwise(x)
+    with pytest.raises(pkg.NoCapableBackendError):
+        pkg.rms_adaln(x, x[:1], x[:1])
+
+
+def test_registry_surface(pkg):
+    backs = pkg.list_backends()
+    assert backs["mi355x"]["available"]
+    assert "int8_linear" in backs["mi355x"]["capabilities"]
+    with pytest.raises(pkg.BackendNotFoundError):
+        with pkg.use_backend("cuda"):
+            pass
+    pkg.disable_backend("mi355x")
+    try:
+        with pytest.raises(pkg.NoCapableBackendError):
+            pkg.registry.get_capable_backend("int8_linear", {})
+        with pytest.raises(pkg.BackendNotFoundError, match="disabled"):
+            pkg.registry.get_implementation("int8_linear", backend="mi355x")
+    finally:
+        pkg.enable_backend("mi355x")
+    with pytest.raises(pkg.BackendNotImplementedError):
+        pkg.registry.get_implementation("scaled_mm_nvfp4", backend="mi355x")
+
+
+def test_unimplemented_reference_features_raise(pkg):
+    from x_minimaxh3_amd import backend
+
+    x = torch.randn(2, 256).bfloat16()
+    w = torch.zeros(8, 256, dtype=torch.int8)
+    with pytest.raises(NotImplementedError, match="ConvRot"):
+        backend.int8_linear(x, w, torch.ones(8), convrot=True)
+    with pytest.raises(NotImplementedError, match="swiglu"):
+        backend.int8_linear(x, w, torch.ones(8), input_act="swiglu")
+    with pytest.raises(ValueError, match="unsupported input_act"):
+        backend.int8_linear(x, w, torch.ones(8), input_act="relu")
+    with pytest.raises(ValueError, match="inner dimensions"):
+        backend.int8_linear(x, torch.zeros(8, 128, dtype=torch.int8), torch.ones(8))
+    with pytest.raises(ValueError, match="per-output-channel"):
+        backend.int8_linear(x, w, torch.ones(3))
+    with pytest.raises(NotImplementedError, match="stochastic"):
+        backend.quantize_int8_rowwise(x, stochastic_rounding=5)
+
+
+def test_w4a8_operand_validation(pkg):
+    from x_minimaxh3_amd import backend
+
+    q = torch.zeros(16, 128, dtype=torch.int8)  # K = 256
+    ok = dict(s_rel=torch.zeros(16, 2), s_channel=torch.zeros(16), codebook=None, correction=None,
+              group_size=128, convrot_groupsize=128)
+    backend.validate_w4a8_operands(q, **ok)
+    with pytest.raises(ValueError, match="s_rel must have shape"):
+        backend.validate_w4a8_operands(q, **{**ok, "s_rel": torch.zeros(16, 3)})
+    with pytest.raises(ValueError, match="s_channel must have shape"):
+        backend.validate_w4a8_operands(q, **{**ok, "s_channel": torch.zeros(15)})
+    with pytest.raises(ValueError, match="divisible by 16"):
+        backend.validate_w4a8_operands(q, **{**ok, "group_size": 24})
+    with pytest.raises(ValueError, match="codebook must have shape"):
+        backend.validate_w4a8_operands(q, **{**ok, "codebook": torch.zeros(8)})
+    with pytest.raises(ValueError, match="2D int8"):
+        backend.validate_w4a8_operands(q.float(), **ok)
+
+
+def test_rope_inplace_guards(pkg):
+    from x_minimaxh3_amd import backend
+
+    qkv = torch.randn(1, 6, 3, 4, 128)
+    q, k = qkv[:, :, 0], qkv[:, :, 1]
+    backend.check_rope_inplace(q, k)              # packed QKV slices interleave, no overlap
+    with pytest.raises(ValueError, match="non-overlapping"):
+        backend.check_rope_inplace(q, q)
+    base = torch.randn(64, 128)
+    with pytest.raises(ValueError, match="internal overlap"):
+        backend.check_rope_inplace(base.as_strided((4, 128), (1, 1)))
+    freqs = torch.randn(1, 6, 1, 64, 2, 2)
+    with pytest.raises(ValueError, match="frequencies or scales"):
+        backend.check_rope_inplace(freqs.view(1, 6, 1, 256)[..., :128], readonly=(freqs,))
+    with pytest.raises(RuntimeError, match="autograd"):
+        backend.check_rope_inplace(torch.randn(2, 8, requires_grad=True))
+
+
+def test_modulation_grouping(pkg):
+    from x_minimaxh3_amd import backend
+
+    x = torch.randn(2, 10, 64)
+    s = torch.randn(2, 1, 64)
+    rows, g = backend._modulation_rows(s, x)
+    assert rows.shape == (2, 64) and g == 10
+    rows, g = backend._modulation_rows(torch.randn(64), x)
+    assert rows.shape == (1, 64) and g == 20
+    rows, g = backend._modulation_rows(torch.randn(1, 10, 64), x)   # broadcast over the outer dim
+    assert rows.shape == (20, 64) and g == 1
+
+
+def test_workloads_deterministic_and_match_oracle_generators(pkg):
+    from x_minimaxh3_amd import workloads
+
+    a = workloads.mlp_inputs(64, 256, 512, n_outlier=4, seed=0, weights="both")
+    b = workloads.mlp_inputs(64, 256, 512, n_outlier=4, seed=0, weights="both")
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+    assert (a["x"][:, a["outliers"]].float().abs().mean() > 5 * a["x"].float().abs().mean())
+    g = torch.Generator().manual_seed(0)
+    torch.randn(64, 256, generator=g)
+    torch.randperm(256, generator=g)
+    w1f = torch.randn(512, 256, generator=g) * 0.02
+    packed, srel, sch = cpu_ref.quantize_w4_weight(w1f, 128)
+    assert torch.equal(a["w1_packed"], packed)
+    assert torch.equal(a["w1_srel"], srel.to(torch.bfloat16))
+    assert torch.equal(a["w1_schannel"], sch)
+    q, s = a["w1"], a["s1"]
+    assert q.dtype == torch.int8 and torch.equal(q, (w1f / s.view(-1, 1)).round().clamp(-128, 127).to(torch.int8))

@@ -1,0 +1,363 @@
+"""GPU parity of the HIP path (through the C ABI) against the CPU oracle.
+
+Bars: int8 codes and int32 accumulators bit-exact; deterministic elementwise
+epilogues (dequant, rotation) bit-exact given identical inputs; bf16 outputs
+that pass through a reduction or a transcendental within max-abs 2e-2 and
+cosine >= 0.9999 (the tolerance the hot path is specified with), with the
+GELU-stage mismatch rate reported.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import cpu_ref
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MIN_COS = 0.9999
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def cos_sim(a, b):
+    return F.cosine_similarity(a.float().flatten(), b.float().flatten(), dim=0).item()
+
+
+def close(got, want, what):
+    got = got.cpu()
+    d = (got.float() - want.float()).abs().max().item() if want.numel() else 0.0
+    c = cos_sim(got, want) if want.numel() and want.float().abs().max() > 0 else 1.0
+    exact = (got == want).float().mean().item() if want.numel() else 1.0
+    say(f"  {what}: max|d|={d:.3e} cos={c:.7f} exact={exact:.5f}")
+    assert d <= MAX_ABS and c >= MIN_COS, (what, d, c)
+
+
+def outlier_acts(m, k, seed=0, n_out=8, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(m, k, generator=g)
+    x[:, torch.randperm(k, generator=g)[:n_out]] *= 20
+    return x.to(dtype)
+
+
+# --------------------------------------------------------------------------- quantizer
+
+@pytest.mark.parametrize("m,k,dtype", [
+    (25200, 5120, torch.bfloat16),   # fc1 input of the 720p MLP
+    (999, 13824, torch.bfloat16),    # fc2 width, ragged rows
+    (37, 1536, torch.float16),
+    (33, 520, torch.float32),
+    (7, 20000, torch.bfloat16),      # wider than the register path
+    (5, 100, torch.bfloat16),        # K not a multiple of 8
+])
+def test_quantize_bit_exact(pkg, dev, m, k, dtype):
+    say(f"quantize m={m} k={k} {dtype}")
+    x = outlier_acts(m, k, seed=m, dtype=dtype)
+    x[0] = 0                                  # zero row -> scale 1e-30, codes 0
+    q, s = pkg.quantize_int8_rowwise(x.to(dev))
+    torch.cuda.synchronize()
+    qr, sr = cpu_ref.quantize_int8_rowwise(x)
+    assert torch.equal(s.cpu(), sr)
+    assert torch.equal(q.cpu(), qr), (q.cpu() != qr).sum().item()
+
+
+def test_quantize_minus_128_cases(pkg, dev):
+    say("quantize -128 cases")
+    vals = torch.arange(0x3f80, 0x4000, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = torch.stack((-vals.float(), vals.float(), vals.float() * 0.5), dim=1).to(torch.bfloat16)
+    q, s = pkg.quantize_int8_rowwise(x.to(dev))
+    qr, sr = cpu_ref.quantize_int8_rowwise(x)
+    assert (qr[:, 0] == -128).any()
+    assert torch.equal(q.cpu(), qr) and torch.equal(s.cpu(), sr)
+
+
+def test_quantize_with_gelu_input_act(pkg, dev):
+    say("quantize gelu input act")
+    from x_minimaxh3_amd import backend
+
+    h = outlier_acts(512, 13824, seed=3) * 0.5
+    q, s = backend._quantize(h.to(dev), 1)
+    torch.cuda.synchronize()
+    g = cpu_ref.gelu_tanh(h)
+    qr, sr = cpu_ref.quantize_int8_rowwise(g)
+    mism = (q.cpu() != qr).float().mean().item()
+    dq = (q.cpu().int() - qr.int()).abs().max().item()
+    say(f"  gelu->int8 code mismatch rate {mism:.2e}, max code delta {dq}")
+    assert torch.allclose(s.cpu(), sr, rtol=2 ** -7, atol=0)
+    assert mism < 1e-3 and dq <= 1
+
+
+# --------------------------------------------------------------------------- GEMM
+
+@pytest.mark.parametrize("m,n,k", [
+    (1024, 6144, 1536),     # the small MLP's fc1
+    (300, 200, 272),        # tails in every dim, K % 128 != 0
+    (256, 256, 128),
+    (1, 16, 16),
+    (777, 5120, 13824),     # fc2 shape, ragged M
+])
+def test_gemm_int32_bit_exact(pkg, dev, m, n, k):
+    say(f"gemm int32 m={m} n={n} k={k}")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8)
+    w = torch.randint(-128, 128, (n, k), generator=g, dtype=torch.int8)
+    a[0] = -128
+    w[0] = -128
+    acc = backend._gemm(a.to(dev), None, w.to(dev), None, None, torch.float32, epilogue=2)
+    torch.cuda.synchronize()
+    assert torch.equal(acc.cpu(), cpu_ref.int8_mm(a, w))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("per_channel,with_bias", [(True, False), (False, True), (True, True)])
+def test_int8_linear_bit_exact(pkg, dev, out_dtype, per_channel, with_bias):
+    say(f"int8_linear {out_dtype} per_channel={per_channel} bias={with_bias}")
+    x = outlier_acts(389, 1536, seed=1)
+    g = torch.Generator().manual_seed(2)
+    w = torch.randint(-127, 128, (640, 1536), generator=g, dtype=torch.int8)
+    sw = torch.rand(640 if per_channel else 1, generator=g) * 1e-3
+    bias = torch.randn(640, generator=g).to(out_dtype) if with_bias else None
+    y = pkg.int8_linear(x.to(dev), w.to(dev), sw.to(dev), None if bias is None else bias.to(dev), out_dtype)
+    torch.cuda.synchronize()
+    yr = cpu_ref.int8_linear(x, w, sw, bias=bias, out_dtype=out_dtype)
+    assert y.dtype == out_dtype
+    assert torch.equal(y.cpu(), yr), (y.cpu() != yr).sum().item()
+
+
+def test_int8_linear_leading_dims_and_strided_input(pkg, dev):
+    say("int8_linear 3D / strided")
+    x = outlier_acts(2 * 65, 512, seed=4).reshape(2, 65, 512)
+    big = torch.zeros(2, 65, 640, dtype=torch.bfloat16)
+    big[..., :512] = x
+    w = torch.randint(-127, 128, (96, 512), dtype=torch.int8)
+    sw = torch.rand(96) * 1e-3
+    y = pkg.int8_linear(big.to(dev)[..., :512], w.to(dev), sw.to(dev))
+    torch.cuda.synchronize()
+    assert y.shape == (2, 65, 96)
+    assert torch.equal(y.cpu(), cpu_ref.int8_linear(x, w, sw))
+
+
+def test_int8_linear_gelu_input_act(pkg, dev):
+    say("int8_linear input_act=gelu_tanh")
+    h = outlier_acts(300, 2048, seed=5) * 0.3
+    w = torch.randint(-127, 128, (256, 2048), dtype=torch.int8)
+    sw = torch.rand(256) * 1e-3
+    y = pkg.int8_linear(h.to(dev), w.to(dev), sw.to(dev), input_act="gelu_tanh")
+    torch.cuda.synchronize()
+    close(y, cpu_ref.int8_linear(h, w, sw, input_act="gelu_tanh"), "int8_linear(gelu)")
+
+
+# --------------------------------------------------------------------------- MLP
+
+def _mlp_stages(pkg, dev, inp):
+    """Run the four MLP kernels one by one through the C ABI and return every
+    intermediate (the fused op runs the same launches)."""
+    from x_minimaxh3_amd import _lib
+
+    x = inp["x"].to(dev)
+    w1, s1, w2, s2 = (inp[k].to(dev) for k in ("w1", "s1", "w2", "s2"))
+    m, d = x.shape
+    f = w1.shape[0]
+    st = _lib.stream_of(x)
+    q1 = torch.empty(m, d, dtype=torch.int8, device=dev)
+    sx = torch.empty(m, dtype=torch.float32, device=dev)
+    g = torch.empty(m, f, dtype=torch.bfloat16, device=dev)
+    amax = torch.full((m,), -1, dtype=torch.int32, device=dev)      # cleared by the quant kernel
+    _lib.call("xmh3_quantize_int8_rowwise_ex", x.data_ptr(), 2, 0, m, d, d, q1.data_ptr(), sx.data_ptr(),
+              amax.data_ptr(), st)
+    _lib.call("xmh3_int8_gemm", q1.data_ptr(), d, w1.data_ptr(), d, m, f, d, sx.data_ptr(), s1.data_ptr(), 1,
+              None, g.data_ptr(), 2, f, 1, amax.data_ptr(), st)
+    q2 = torch.empty(m, f, dtype=torch.int8, device=dev)
+    sg = torch.empty(m, dtype=torch.float32, device=dev)
+    _lib.call("xmh3_requant_int8_rows", g.data_ptr(), 2, m, f, f, amax.data_ptr(), q2.data_ptr(), sg.data_ptr(), st)
+    y = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    _lib.call("xmh3_int8_gemm", q2.data_ptr(), f, w2.data_ptr(), f, m, d, f, sg.data_ptr(), s2.data_ptr(), 1,
+              None, y.data_ptr(), 2, d, 0, None, st)
+    torch.cuda.synchronize()
+    return {"q1": q1.cpu(), "sx": sx.cpu(), "g": g.cpu(), "amax": amax.cpu().view(torch.float32),
+            "q2": q2.cpu(), "sg": sg.cpu(), "y": y.cpu()}
+
+
+def test_mlp_small_stagewise(pkg, dev):
+    say("w8a8 mlp 1024x1536x6144 stagewise")
+    from x_minimaxh3_amd import workloads
+
+    inp = workloads.mlp_inputs(**workloads.CONFIGS["mlp_small"], seed=0)
+    st = _mlp_stages(pkg, dev, inp)
+    yr, p = cpu_ref.w8a8_mlp(inp["x"], inp["w1"], inp["s1"], inp["w2"], inp["s2"], return_parts=True)
+    assert torch.equal(st["q1"], p["q1"]) and torch.equal(st["sx"], p["s1"].reshape(-1))
+    # fc1 epilogue: h = bf16(acc*(sx*sw)) is exact; g = bf16(gelu(h)) uses the device tanh
+    g_ref = cpu_ref.gelu_tanh(p["h"])
+    gm = (st["g"] != g_ref).float().mean().item()
+    ulp = cpu_ref.bf16_ulp_diff(st["g"], g_ref)
+    big = g_ref.float().abs() > 1e-3
+    say(f"  gelu stage: mismatch rate {gm:.2e}, max ulp (|g|>1e-3) {ulp[big].max().item():.1f}")
+    assert ulp[big].max().item() <= 1.0 and gm < 1e-2
+    # row amax is exactly max|g| of the GPU's own g
+    assert torch.equal(st["amax"], st["g"].float().abs().amax(dim=1))
+    # requant of the GPU's g is bit-exact against the oracle quantizer on that g
+    q2r, s2r = cpu_ref.quantize_int8_rowwise(st["g"])
+    assert torch.equal(st["q2"], q2r) and torch.equal(st["sg"], s2r.reshape(-1))
+    # fc2 + dequant bit-exact given the GPU's q2
+    yr2 = cpu_ref.dequant(cpu_ref.int8_mm(st["q2"], inp["w2"]), st["sg"], inp["s2"])
+    assert torch.equal(st["y"], yr2)
+    q2_mism = (st["q2"] != p["q2"]).float().mean().item()
+    say(f"  requant code mismatch vs oracle end-to-end: {q2_mism:.2e}")
+    close(st["y"], yr, "mlp output")
+
+
+def test_mlp_fused_op_small(pkg, dev):
+    say("w8a8 mlp fused op 1024x1536x6144")
+    from x_minimaxh3_amd import workloads
+
+    inp = workloads.mlp_inputs(**workloads.CONFIGS["mlp_small"], seed=0)
+    y = pkg.w8a8_mlp(*(inp[k].to(dev) for k in ("x", "w1", "s1", "w2", "s2")))
+    torch.cuda.synchronize()
+    st = _mlp_stages(pkg, dev, inp)
+    assert torch.equal(y.cpu(), st["y"])       # the fused op runs the same kernels
+    close(y, cpu_ref.w8a8_mlp(inp["x"], inp["w1"], inp["s1"], inp["w2"], inp["s2"]), "fused mlp")
+
+
+def test_mlp_720p_row_sample(pkg, dev):
+    """Full 720p shape on the GPU; rows are independent (per-token quant), so
+    the oracle checks a sample of rows including the partial last tile."""
+    say("w8a8 mlp 25200x5120x13824")
+    from x_minimaxh3_amd import workloads
+
+    inp = workloads.mlp_inputs(**workloads.CONFIGS["mlp_720p"], seed=0)
+    y = pkg.w8a8_mlp(*(inp[k].to(dev) for k in ("x", "w1", "s1", "w2", "s2"))).cpu()
+    g = torch.Generator().manual_seed(1)
+    rows = torch.cat((torch.randperm(25200 - 200, generator=g)[:200], torch.arange(25200 - 200, 25200)))
+    yr = cpu_ref.w8a8_mlp(inp["x"][rows], inp["w1"], inp["s1"], inp["w2"], inp["s2"])
+    close(y[rows], yr, "720p mlp rows")
+    assert torch.isfinite(y.float()).all()
+
+
+def test_w4_decode_bit_exact(pkg, dev):
+    say("w4 decode")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(8)
+    w = torch.randn(384, 1024, generator=g) * 0.02
+    for gs in (128, 16, 8):
+        packed, srel, _ = cpu_ref.quantize_w4_weight(w, gs)
+        for srel_t in (srel, srel.to(torch.bfloat16)):
+            out = backend.dequant_int4_grouped_to_int8(packed.to(dev), srel_t.to(dev), None, gs)
+            torch.cuda.synchronize()
+            assert torch.equal(out.cpu(), cpu_ref.dequant_int4_grouped_to_int8(packed, srel_t.float(), gs))
+    cb = torch.linspace(-1, 1, 16) * 7.3
+    packed, srel, _ = cpu_ref.quantize_w4_weight(w, 128)
+    out = backend.dequant_int4_grouped_to_int8(packed.to(dev), srel.to(dev), cb.to(dev), 128)
+    assert torch.equal(out.cpu(), cpu_ref.dequant_int4_grouped_to_int8(packed, srel, 128, codebook=cb))
+
+
+def test_w4a8_linear_and_mlp(pkg, dev):
+    say("w4a8 linear + mlp 1024x1536x6144")
+    from x_minimaxh3_amd import workloads
+
+    inp = workloads.mlp_inputs(**workloads.CONFIGS["mlp_small"], seed=0, weights="w4a8")
+    x = inp["x"]
+    y = pkg.w4a8_int8_linear(x.to(dev), inp["w1_packed"].to(dev), inp["w1_srel"].to(dev),
+                             inp["w1_schannel"].to(dev), group_size=128, convrot_groupsize=128, convrot=False)
+    torch.cuda.synchronize()
+    yr = cpu_ref.w4a8_linear(x, inp["w1_packed"], inp["w1_srel"].float(), inp["w1_schannel"], 128)
+    assert torch.equal(y.cpu(), yr)
+    ym = pkg.w4a8_mlp(x.to(dev), *(inp[k].to(dev) for k in ("w1_packed", "w1_srel", "w1_schannel",
+                                                             "w2_packed", "w2_srel", "w2_schannel")), 128)
+    torch.cuda.synchronize()
+    ymr = cpu_ref.w4a8_mlp(x, inp["w1_packed"], inp["w1_srel"].float(), inp["w1_schannel"],
+                           inp["w2_packed"], inp["w2_srel"].float(), inp["w2_schannel"], 128)
+    close(ym, ymr, "w4a8 mlp")
+
+
+# --------------------------------------------------------------------------- norm / rope
+
+def test_norm_rope_720p(pkg, dev):
+    say("norm_rope 25200x5120")
+    from x_minimaxh3_amd import workloads
+
+    nr = workloads.norm_rope_inputs(grid=(7, 45, 80))
+    qo, ko = pkg.norm_rope(nr["q"].to(dev), nr["k"].to(dev), nr["scale"].to(dev), nr["shift"].to(dev),
+                           nr["freqs"].to(dev), nr["eps"], 128)
+    torch.cuda.synchronize()
+    for got, x, name in ((qo, nr["q"], "Q"), (ko, nr["k"], "K")):
+        want = cpu_ref.norm_rope(x, nr["scale"], nr["shift"], nr["freqs"], 128, nr["eps"])
+        close(got, want, f"norm_rope {name}")
+
+
+def test_rope_only_bit_exact(pkg, dev):
+    say("apply_rope_split_half fp32 + bf16 tables")
+    g = torch.Generator().manual_seed(21)
+    xq = torch.randn(2, 50, 8, 128, generator=g).to(torch.bfloat16)
+    xk = torch.randn(2, 50, 8, 128, generator=g).to(torch.bfloat16)
+    ang = torch.rand(1, 50, 1, 64, generator=g) * 50
+    c, s = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -s, s, c), -1).reshape(1, 50, 1, 64, 2, 2)
+    for t in (tab, tab.to(torch.bfloat16)):
+        oq, ok = pkg.apply_rope_split_half(xq.to(dev), xk.to(dev), t.to(dev))
+        torch.cuda.synchronize()
+        assert torch.equal(oq.cpu(), cpu_ref.apply_rope_split_half1(xq, t))
+        assert torch.equal(ok.cpu(), cpu_ref.apply_rope_split_half1(xk, t))
+    q2 = xq.to(dev).clone()
+    k2 = xk.to(dev).clone()
+    pkg.apply_rope_split_half_(q2, k2, tab.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(q2.cpu(), cpu_ref.apply_rope_split_half1(xq, tab))
+
+
+def test_h3_qknorm_rope_partial_inplace(pkg, dev):
+    """H3 call form: per-head RMSNorm with weight, eps 1e-5, partial rotary 96
+    of 128 with a bf16 table, in place on views of a packed QKV tensor."""
+    say("rms_rope_split_half_ rot 96 bf16 table, packed qkv views")
+    g = torch.Generator().manual_seed(22)
+    S, H, D = 333, 6, 128
+    qkv = torch.randn(1, S, 3, H, D, generator=g).to(torch.bfloat16)
+    ang = torch.rand(1, S, 1, 48, generator=g) * 30
+    c, s = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -s, s, c), -1).reshape(1, S, 1, 48, 2, 2).to(torch.bfloat16)
+    qw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    dq = qkv.to(dev)
+    pkg.rms_rope_split_half_(dq[:, :, 0], dq[:, :, 1], tab.to(dev), qw.to(dev), kw.to(dev), 1e-5, 96)
+    torch.cuda.synchronize()
+    out = dq.cpu()
+    wq = cpu_ref.rms_rope_split_half1(qkv[:, :, 0], tab, qw, 1e-5, 96)
+    wk = cpu_ref.rms_rope_split_half1(qkv[:, :, 1], tab, kw, 1e-5, 96)
+    close(out[:, :, 0], wq, "q")
+    close(out[:, :, 1], wk, "k")
+    assert torch.equal(out[:, :, 2], qkv[:, :, 2])    # v untouched
+
+
+@pytest.mark.parametrize("mod_dtype", [torch.bfloat16, torch.float32])
+def test_rms_adaln(pkg, dev, mod_dtype):
+    say(f"rms_adaln scale/shift {mod_dtype}")
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(2, 300, 5120, generator=g).to(torch.bfloat16)
+    sc = (torch.randn(2, 1, 5120, generator=g) * 0.1).to(mod_dtype)
+    sh = (torch.randn(2, 1, 5120, generator=g) * 0.1).to(mod_dtype)
+    out = pkg.rms_adaln(x.to(dev), sc.to(dev), sh.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    want = cpu_ref.rms_adaln(x, sc, sh, 1e-6)
+    assert out.dtype == want.dtype
+    close(out, want, "rms_adaln")
+
+
+def test_h3_segmented_rms_adaln(pkg, dev):
+    say("h3 segmented rms_adaln")
+    from x_minimaxh3_amd import h3
+
+    g = torch.Generator().manual_seed(24)
+    x = torch.randn(1000, 1024, generator=g).to(torch.bfloat16)
+    w = (torch.rand(1024, generator=g) + 0.5).to(torch.bfloat16)
+    sc = (torch.randn(3, 1024, generator=g) * 0.1).to(torch.bfloat16)
+    sh = (torch.randn(3, 1024, generator=g) * 0.1).to(torch.bfloat16)
+    segs = ((0, 77, 0), (77, 200, 1), (200, 1000, 2))
+    out = h3.rms_adaln(x.to(dev), w.to(dev), sh.to(dev), sc.to(dev), segs, eps=1e-5)
+    torch.cuda.synchronize()
+    close(out, cpu_ref.rms_adaln_segmented(x, w, sh, sc, segs, eps=1e-5), "segmented rms_adaln")

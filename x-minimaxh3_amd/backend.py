@@ -1,0 +1,609 @@
+"""The ``"mi355x"`` backend: reference-signature implementations over the C ABI.
+
+Each function has the name, argument meaning, defaults and error behaviour of
+the reference backend function it replaces (CK = backends/turbo/vendor/
+comfy_kitchen): validation raises ``ValueError`` with the reference's
+conditions; work goes to the HIP library on the tensors' current stream; there
+is no CPU path. Features the reference has but this backend does not
+implement (ConvRot rotation, stochastic rounding, swiglu input act, the
+asymmetric W4A8 correction) raise ``NotImplementedError`` instead of returning
+different numbers.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import DTYPE_CODE, call, ptr, stream_of
+from .registry import (
+    ExactDims,
+    FunctionConstraints,
+    MinDims,
+    ParamConstraint,
+    ValidationResult,
+    registry,
+)
+
+FLOATS = frozenset({torch.float32, torch.float16, torch.bfloat16})
+HALFS = frozenset({torch.float16, torch.bfloat16})
+
+
+def _rows(x: torch.Tensor) -> tuple[torch.Tensor, int, int, int]:
+    """[..., K] -> (2D [M, K] view or copy, M, K, row stride); the last dim is
+    made contiguous and rows evenly strided."""
+    k = x.shape[-1]
+    x2 = x.reshape(-1, k)
+    if k > 1 and x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    ld = x2.stride(0) if x2.shape[0] > 1 else k
+    if ld < k:
+        x2, ld = x2.contiguous(), k
+    return x2, x2.shape[0], k, ld
+
+
+def _aligned_rows(x: torch.Tensor) -> tuple[torch.Tensor, int, int, int]:
+    """As _rows, preferring the kernels' 16-byte vector path: rows whose
+    stride or base is not 16-byte aligned are copied to a contiguous tensor."""
+    x2, m, k, ld = _rows(x)
+    if (ld * x2.element_size()) % 16 or x2.data_ptr() % 16:
+        x2, ld = x2.contiguous(), k
+    return x2, m, k, ld
+
+
+# --------------------------------------------------------------------------- quantization
+
+def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0):
+    """CK/backends/eager/quantization.py:857-875 -> (int8 like x, fp32 [..., 1])."""
+    if stochastic_rounding is not None and stochastic_rounding > 0:
+        raise NotImplementedError("stochastic rounding is not implemented by the mi355x backend")
+    return _quantize(x, 0)
+
+
+def _quantize(x: torch.Tensor, act: int):
+    x2, m, k, ld = _aligned_rows(x)
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(*x.shape[:-1], 1, dtype=torch.float32, device=x.device)
+    if m and k:
+        call("xmh3_quantize_int8_rowwise", x2.data_ptr(), DTYPE_CODE[x.dtype], act, m, k, ld,
+             q.data_ptr(), s.data_ptr(), stream_of(x))
+    elif m:
+        s.fill_(1e-30)
+    return q, s
+
+
+_ACT = {None: 0, "none": 0, "gelu_tanh": 1}
+
+
+def _act_code(input_act):
+    if input_act == "swiglu":
+        raise NotImplementedError("input_act='swiglu' is not implemented by the mi355x backend")
+    if input_act not in _ACT:
+        known = ["gelu_tanh", "none", "swiglu"]
+        raise ValueError(f"unsupported input_act: {input_act!r} (expected one of {known})")
+    return _ACT[input_act]
+
+
+def _gemm(q: torch.Tensor, sx: torch.Tensor, weight: torch.Tensor, ws: torch.Tensor,
+          bias: torch.Tensor | None, out_dtype: torch.dtype, epilogue: int = 0) -> torch.Tensor:
+    m, k = q.shape
+    n = weight.shape[0]
+    if k % 16:
+        kp = (k + 15) // 16 * 16
+        q = torch.nn.functional.pad(q, (0, kp - k))
+        weight = torch.nn.functional.pad(weight, (0, kp - k))
+        k = kp
+    weight = weight.contiguous()
+    out = torch.empty(m, n, dtype=torch.int32 if epilogue == 2 else out_dtype, device=q.device)
+    if bias is not None:
+        bias = bias.to(device=q.device, dtype=out_dtype).contiguous().reshape(-1)
+    if m and n:
+        call("xmh3_int8_gemm", q.data_ptr(), q.stride(0), weight.data_ptr(), weight.stride(0), m, n, k,
+             ptr(sx), ptr(ws), int(ws is not None and ws.numel() != 1), ptr(bias), out.data_ptr(),
+             DTYPE_CODE.get(out_dtype, 0), out.stride(0), epilogue, None, stream_of(q))
+    return out
+
+
+def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                convrot: bool = False, convrot_groupsize: int = 256, input_act: str | None = None):
+    """CK/backends/eager/quantization.py:971-1056 (convrot=False):
+    act -> per-row int8 quant -> MFMA int8 GEMM with the fp32 dequant epilogue."""
+    if convrot:
+        raise NotImplementedError("ConvRot online rotation is not implemented by the mi355x backend")
+    act = _act_code(input_act)
+    if out_dtype is None:
+        out_dtype = torch.bfloat16
+    if x.shape[-1] != weight.shape[-1]:
+        raise ValueError(
+            f"Input and weight inner dimensions must match, got {x.shape[-1]} and {weight.shape[-1]}")
+    weight = weight.to(device=x.device)
+    ws = weight_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
+    if ws.numel() not in (1, weight.shape[0]):
+        raise ValueError(
+            f"INT8 weight scale must be scalar or per-output-channel, got {tuple(weight_scale.shape)} "
+            f"for weight shape {tuple(weight.shape)}")
+    lead = x.shape[:-1]
+    q, sx = _quantize(x.reshape(-1, x.shape[-1]), act)
+    out = _gemm(q, sx, weight, ws, bias, out_dtype)
+    return out.reshape(*lead, weight.shape[0])
+
+
+# --------------------------------------------------------------------------- W4A8
+
+def validate_w4a8_operands(qdata, s_rel, s_channel, codebook, correction, group_size, convrot_groupsize):
+    """The operand rules of CK/backends/eager/w4a8_int8.py:366-404."""
+    if qdata.dim() != 2 or qdata.dtype != torch.int8:
+        raise ValueError("packed weight must be a 2D int8 tensor")
+    n, k_half = qdata.shape
+    k = k_half * 2
+    if (group_size < 4 or k % 16 != 0 or k % group_size != 0 or k % convrot_groupsize != 0
+            or (16 % group_size != 0 and group_size % 16 != 0)):
+        raise ValueError(
+            f"K={k} must be divisible by 16, group_size={group_size}, and "
+            f"convrot_groupsize={convrot_groupsize}; group_size must be >=4 "
+            f"and divide 16 or be a multiple of 16")
+    groups = k // group_size
+    if tuple(s_rel.shape) != (n, groups):
+        raise ValueError(f"s_rel must have shape {(n, groups)}, got {tuple(s_rel.shape)}")
+    if tuple(s_channel.shape) != (n,):
+        raise ValueError(f"s_channel must have shape {(n,)}, got {tuple(s_channel.shape)}")
+    if correction is not None and tuple(correction.shape) != (groups, n):
+        raise ValueError(f"correction must have shape {(groups, n)}, got {tuple(correction.shape)}")
+    if codebook is not None and tuple(codebook.shape) != (16,):
+        raise ValueError(f"codebook must have shape (16,), got {tuple(codebook.shape)}")
+
+
+def _srel_for_kernel(s_rel: torch.Tensor) -> tuple[torch.Tensor, int]:
+    if s_rel.dtype == torch.bfloat16:
+        return s_rel.contiguous(), 2
+    if s_rel.dtype == torch.float32:
+        return s_rel.contiguous(), 0
+    # e.g. float8_e4m3fn: widen exactly to fp32 (every fp8/fp16 value is an fp32)
+    return s_rel.to(torch.float32).contiguous(), 0
+
+
+def dequant_int4_grouped_to_int8(qdata: torch.Tensor, s_rel: torch.Tensor, codebook: torch.Tensor | None,
+                                 group_size: int) -> torch.Tensor:
+    """CK/backends/eager/w4a8_int8.py:344-363 on the GPU."""
+    n, kh = qdata.shape
+    k = kh * 2
+    out = torch.empty(n, k, dtype=torch.int8, device=qdata.device)
+    srel, code = _srel_for_kernel(s_rel)
+    cb = None if codebook is None else codebook.to(device=qdata.device, dtype=torch.float32).contiguous()
+    qd = qdata.contiguous()
+    if n and k:
+        call("xmh3_w4_decode_int8", qd.data_ptr(), srel.data_ptr(), code, ptr(cb), n, k, group_size,
+             out.data_ptr(), stream_of(qdata))
+    return out
+
+
+def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, s_channel: torch.Tensor,
+                     codebook: torch.Tensor | None = None, correction: torch.Tensor | None = None,
+                     bias: torch.Tensor | None = None, group_size: int = 16, convrot_groupsize: int = 256,
+                     out_dtype: torch.dtype = torch.bfloat16, convrot: bool = True):
+    """CK/backends/eager/w4a8_int8.py:457-508: decode the grouped int4 storage
+    to the int8 grid, then int8_linear with s_channel as the per-channel scale.
+    The reference always rotates (ConvRot); ``convrot=False`` selects the
+    unrotated form used by the GELU MLP workloads."""
+    validate_w4a8_operands(qdata, s_rel, s_channel, codebook, correction, group_size, convrot_groupsize)
+    if x.shape[-1] != qdata.shape[-1] * 2:
+        raise ValueError(f"Input K={x.shape[-1]} does not match qdata K={qdata.shape[-1] * 2}")
+    if correction is not None:
+        raise NotImplementedError("asymmetric W4A8 (correction) is not implemented by the mi355x backend")
+    if convrot:
+        raise NotImplementedError("ConvRot online rotation is not implemented by the mi355x backend")
+    w8 = dequant_int4_grouped_to_int8(qdata, s_rel, codebook, group_size)
+    return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype)
+
+
+# --------------------------------------------------------------------------- MLP blocks
+
+def w8a8_mlp(x: torch.Tensor, w1: torch.Tensor, s1: torch.Tensor, w2: torch.Tensor, s2: torch.Tensor,
+             out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """y = int8_linear(int8_linear(x, w1, s1), w2, s2, input_act="gelu_tanh")
+    as four fused kernels (see csrc/mlp.hip)."""
+    d = x.shape[-1]
+    f = w1.shape[0]
+    if tuple(w1.shape) != (f, d) or tuple(w2.shape) != (d, f):
+        raise ValueError(f"w1 must be [F, D] and w2 [D, F], got {tuple(w1.shape)} and {tuple(w2.shape)}")
+    s1 = s1.to(torch.float32).reshape(-1).contiguous()
+    s2 = s2.to(torch.float32).reshape(-1).contiguous()
+    if s1.numel() not in (1, f) or s2.numel() not in (1, d):
+        raise ValueError("weight scales must be scalar or per-output-channel")
+    x2, m, _, ldx = _aligned_rows(x)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], d, dtype=torch.bfloat16, device=x.device)
+    y2 = out.reshape(-1, d)
+    nbytes = _lib.query("xmh3_w8a8_mlp_workspace_bytes", m, d, f)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    if m:
+        call("xmh3_w8a8_mlp", x2.data_ptr(), DTYPE_CODE[x.dtype], m, d, f, ldx, w1.contiguous().data_ptr(),
+             s1.data_ptr(), int(s1.numel() != 1), w2.contiguous().data_ptr(), s2.data_ptr(),
+             int(s2.numel() != 1), y2.data_ptr(), y2.stride(0), workspace.data_ptr(), workspace.numel(),
+             stream_of(x))
+    return out
+
+
+def w4a8_mlp(x: torch.Tensor, w1_packed: torch.Tensor, w1_srel: torch.Tensor, w1_schannel: torch.Tensor,
+             w2_packed: torch.Tensor, w2_srel: torch.Tensor, w2_schannel: torch.Tensor,
+             group_size: int = 128, out: torch.Tensor | None = None,
+             workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The W4A8 GELU MLP: both weights grouped int4 (uniform levels, no
+    rotation), decoded to the int8 grid on the GPU, then the W8A8 chain."""
+    d = x.shape[-1]
+    f = w1_packed.shape[0]
+    validate_w4a8_operands(w1_packed, w1_srel, w1_schannel, None, None, group_size, group_size)
+    validate_w4a8_operands(w2_packed, w2_srel, w2_schannel, None, None, group_size, group_size)
+    if w1_packed.shape[1] * 2 != d or tuple(w2_packed.shape) != (d, f // 2):
+        raise ValueError("w1_packed must be [F, D/2] and w2_packed [D, F/2]")
+    if w1_srel.dtype != w2_srel.dtype:
+        raise ValueError("both s_rel tensors must have the same dtype")
+    s1, code = _srel_for_kernel(w1_srel)
+    s2, _ = _srel_for_kernel(w2_srel)
+    x2, m, _, ldx = _aligned_rows(x)
+    if out is None:
+        out = torch.empty(*x.shape[:-1], d, dtype=torch.bfloat16, device=x.device)
+    y2 = out.reshape(-1, d)
+    nbytes = _lib.query("xmh3_w4a8_mlp_workspace_bytes", m, d, f)
+    if workspace is None or workspace.numel() < nbytes:
+        workspace = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    if m:
+        call("xmh3_w4a8_mlp", x2.data_ptr(), DTYPE_CODE[x.dtype], m, d, f, ldx,
+             w1_packed.contiguous().data_ptr(), s1.data_ptr(), w1_schannel.float().contiguous().data_ptr(),
+             w2_packed.contiguous().data_ptr(), s2.data_ptr(), w2_schannel.float().contiguous().data_ptr(),
+             code, group_size, y2.data_ptr(), y2.stride(0), workspace.data_ptr(), workspace.numel(),
+             stream_of(x))
+    return out
+
+
+# --------------------------------------------------------------------------- AdaLN / RoPE
+
+def _modulation_rows(t: torch.Tensor, x: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """Reduce a scale/shift tensor broadcastable to x [..., D] to distinct rows
+    [R, D] plus the group size G such that token row r uses row r // G. Falls
+    back to materialising the broadcast (G = 1) when the kept dims are not
+    outer to the broadcast dims (the grouping rule of CK/backends/_modulation.py:12-57)."""
+    d = x.shape[-1]
+    n = x.numel() // d if d else 0
+    if t.shape[-1] == d and t.dim() <= x.dim():
+        lead_t = (1,) * (x.dim() - t.dim()) + tuple(t.shape[:-1])
+        lead_x = tuple(x.shape[:-1])
+        ok, seen_bcast = True, False
+        for st, sx in zip(lead_t, lead_x):
+            if st == sx:
+                if sx != 1 and seen_bcast:
+                    ok = False
+                    break
+            elif st == 1:
+                seen_bcast = seen_bcast or sx != 1
+            else:
+                ok = False
+                break
+        rows = t.numel() // d if d else 0
+        if ok and rows > 0 and n % rows == 0:
+            return t.reshape(rows, d).contiguous(), n // rows
+    return t.expand_as(x).reshape(n, d).contiguous(), 1
+
+
+def rms_adaln(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """CK/backends/eager/adaln.py:17-20: rms_norm(x) * (1 + scale) + shift."""
+    if scale.dtype != shift.dtype:
+        raise NotImplementedError("scale and shift with different dtypes are not supported by the mi355x backend")
+    out_dtype = torch.promote_types(x.dtype, scale.dtype)
+    d = x.shape[-1]
+    x2, m, _, ld = _aligned_rows(x)
+    sc, g1 = _modulation_rows(scale.to(x.device), x)
+    sh, g2 = _modulation_rows(shift.to(x.device), x)
+    if g1 != g2 or sc.shape != sh.shape:
+        sc, g1 = scale.expand_as(x).reshape(m, d).contiguous(), 1
+        sh = shift.expand_as(x).reshape(m, d).contiguous()
+    out = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    if m:
+        call("xmh3_rms_adaln", x2.data_ptr(), out.data_ptr(), DTYPE_CODE[x.dtype], m, d, ld, d, None,
+             sc.data_ptr(), sh.data_ptr(), DTYPE_CODE[sc.dtype], sc.stride(0), None, g1, float(eps),
+             stream_of(x))
+    return out
+
+
+def rms_adaln_rows(x: torch.Tensor, norm_weight: torch.Tensor | None, scale_rows: torch.Tensor,
+                   shift_rows: torch.Tensor, row_map: torch.Tensor, eps: float) -> torch.Tensor:
+    """Segmented form: out[t] = rms_norm(x[t], weight) * (1 + scale[row_map[t]]) + shift[row_map[t]]
+    with scale/shift already in x's dtype (h3serve/native_engine/model/kernels.py:7623-7634)."""
+    x2, m, d, ld = _aligned_rows(x)
+    out = torch.empty(m, d, dtype=x.dtype, device=x.device)
+    w = None if norm_weight is None else norm_weight.to(device=x.device, dtype=x.dtype).contiguous()
+    sc = scale_rows.to(device=x.device, dtype=x.dtype).contiguous()
+    sh = shift_rows.to(device=x.device, dtype=x.dtype).contiguous()
+    rm = row_map.to(device=x.device, dtype=torch.int32).contiguous()
+    if m:
+        call("xmh3_rms_adaln", x2.data_ptr(), out.data_ptr(), DTYPE_CODE[x.dtype], m, d, ld, d, ptr(w),
+             sc.data_ptr(), sh.data_ptr(), DTYPE_CODE[x.dtype], sc.stride(0), rm.data_ptr(), 1, float(eps),
+             stream_of(x))
+    return out
+
+
+def _freq_strides(x: torch.Tensor, freqs: torch.Tensor, rot: int) -> tuple[torch.Tensor, list[int]]:
+    """Broadcast strides of a [..., rot/2, 2, 2] table over x's (B, S, H)."""
+    if freqs.dim() < 3 or tuple(freqs.shape[-3:]) != (rot // 2, 2, 2):
+        raise ValueError(f"freqs_cis must end with ({rot // 2}, 2, 2), got {tuple(freqs.shape)}")
+    f = freqs
+    # the reference trims a longer sequence dim (CK/_rope_utils.py:4-13)
+    if x.dim() > 2 and f.dim() > 2 and x.shape[2] != 1 and f.dim() == 6 and f.shape[2] > x.shape[2]:
+        f = f[:, :, : x.shape[2]]
+    lead = f.shape[:-3]
+    if f.stride(-1) != 1 or f.stride(-2) != 2 or f.stride(-3) != 4:
+        f = f.contiguous()
+    xlead = x.shape[:-1]
+    if len(lead) > len(xlead):
+        if any(s != 1 for s in lead[: len(lead) - len(xlead)]):
+            raise ValueError("freqs_cis has more leading dims than the input")
+        f = f.reshape(*lead[len(lead) - len(xlead):], *f.shape[-3:])
+        lead = f.shape[:-3]
+    pad = len(xlead) - len(lead)
+    strides = [0] * pad + [f.stride(i) if f.shape[i] != 1 else 0 for i in range(len(lead))]
+    sizes = [1] * pad + list(lead)
+    for s_f, s_x in zip(sizes, xlead):
+        if s_f not in (1, s_x):
+            raise ValueError(f"freqs_cis shape {tuple(freqs.shape)} does not broadcast to {tuple(x.shape)}")
+    # fold to 3 leading dims (B, S, H)
+    while len(strides) < 3:
+        strides.insert(0, 0)
+    if len(strides) > 3:
+        raise ValueError("inputs with more than 3 leading dims are not supported")
+    return f, strides
+
+
+def _bsh(x: torch.Tensor) -> tuple[list[int], list[int]]:
+    if x.dim() < 2 or x.dim() > 4:
+        raise ValueError(f"expected a 2D-4D [..., head_dim] tensor, got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        raise ValueError("head_dim must be the contiguous dim")
+    sizes = list(x.shape[:-1])
+    strides = list(x.stride()[:-1])
+    while len(sizes) < 3:
+        sizes.insert(0, 1)
+        strides.insert(0, 0)
+    return sizes, strides
+
+
+def _rope_call(x: torch.Tensor, out: torch.Tensor, freqs: torch.Tensor, weight: torch.Tensor | None,
+               eps: float, rot_dim: int, norm: bool) -> None:
+    d = x.shape[-1]
+    rot = rot_dim if rot_dim else d
+    f, fstr = _freq_strides(x, freqs, rot)
+    sizes, xstr = _bsh(x)
+    _, ostr = _bsh(out)
+    w = None
+    wcode = 0
+    if norm:
+        w = weight.to(device=x.device).contiguous()
+        if w.dtype != x.dtype:
+            w = w.to(x.dtype) if w.dtype != torch.float32 else w
+        wcode = DTYPE_CODE[w.dtype]
+    b, s, h = sizes
+    if x.numel():
+        call("xmh3_rope_split_half", x.data_ptr(), out.data_ptr(), DTYPE_CODE[x.dtype], b, s, h, d,
+             _lib.i64array(xstr), _lib.i64array(ostr), ptr(w), wcode, f.data_ptr(), DTYPE_CODE[f.dtype],
+             _lib.i64array(fstr), rot if rot_dim else 0, float(eps), int(norm), stream_of(x))
+
+
+def apply_rope_split_half1(x: torch.Tensor, freqs_cis: torch.Tensor) -> torch.Tensor:
+    """CK/backends/eager/rope.py:39-42."""
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _rope_call(x, out, freqs_cis.to(x.device), None, 0.0, 0, False)
+    return out
+
+
+def apply_rope_split_half(xq, xk, freqs_cis):
+    return apply_rope_split_half1(xq, freqs_cis), apply_rope_split_half1(xk, freqs_cis)
+
+
+def apply_rope_split_half1_(x, freqs_cis):
+    check_rope_inplace(x, readonly=(freqs_cis,))
+    _rope_call(x, x, freqs_cis, None, 0.0, 0, False)
+    return x
+
+
+def apply_rope_split_half_(xq, xk, freqs_cis):
+    check_rope_inplace(xq, xk, readonly=(freqs_cis,))
+    _rope_call(xq, xq, freqs_cis, None, 0.0, 0, False)
+    _rope_call(xk, xk, freqs_cis, None, 0.0, 0, False)
+    return xq, xk
+
+
+def rms_rope_split_half1(x, freqs_cis, scale, epsilon=1e-6, rot_dim=0):
+    """CK/backends/eager/rope.py:67-92 (split_half=True)."""
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _rope_call(x, out, freqs_cis, scale, epsilon, rot_dim, True)
+    return out
+
+
+def rms_rope_split_half(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6, rot_dim=0):
+    if k_scale is None:
+        k_scale = q_scale
+    return (rms_rope_split_half1(q, freqs_cis, q_scale, epsilon, rot_dim),
+            rms_rope_split_half1(k, freqs_cis, k_scale, epsilon, rot_dim))
+
+
+def rms_rope_split_half1_(x, freqs_cis, scale, epsilon=1e-6, rot_dim=0):
+    check_rope_inplace(x, readonly=(freqs_cis, scale))
+    _rope_call(x, x, freqs_cis, scale, epsilon, rot_dim, True)
+    return x
+
+
+def rms_rope_split_half_(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6, rot_dim=0):
+    """In place (CK/backends/eager/rope.py:178-189)."""
+    if k_scale is None:
+        k_scale = q_scale
+    check_rope_inplace(q, k, readonly=(freqs_cis, q_scale, k_scale))
+    _rope_call(q, q, freqs_cis, q_scale, epsilon, rot_dim, True)
+    _rope_call(k, k, freqs_cis, k_scale, epsilon, rot_dim, True)
+    return q, k
+
+
+def norm_rope(q: torch.Tensor, k: torch.Tensor | None, scale: torch.Tensor, shift: torch.Tensor,
+              freqs_cis: torch.Tensor, eps: float = 1e-6, head_dim: int = 128,
+              inplace: bool = False):
+    """Fused rms_adaln (RMS over the full row) + split-half RoPE per head for
+    Q and K of the same tokens. q/k: [..., tokens, width]; scale/shift rows
+    broadcast over tokens; freqs: [1, tokens or 1, 1, head_dim/2, 2, 2]."""
+    width = q.shape[-1]
+    if width % head_dim:
+        raise ValueError(f"width {width} is not a multiple of head_dim {head_dim}")
+    if k is not None and k.shape != q.shape:
+        raise ValueError("q and k must have the same shape")
+    if scale.dtype != q.dtype or shift.dtype != q.dtype:
+        raise ValueError("scale and shift must have q's dtype")
+    q2, m, _, ldq = _aligned_rows(q)
+    k2 = None
+    if k is not None:
+        k2, _, _, ldk = _aligned_rows(k)
+        if ldk != ldq:
+            q2, k2, ldq = q2.contiguous(), k2.contiguous(), width
+    sc, g1 = _modulation_rows(scale, q.reshape(m, width))
+    sh, g2 = _modulation_rows(shift, q.reshape(m, width))
+    if g1 != g2:
+        raise ValueError("scale and shift must broadcast the same way")
+    f = freqs_cis
+    if tuple(f.shape[-3:]) != (head_dim // 2, 2, 2):
+        raise ValueError(f"freqs_cis must end with ({head_dim // 2}, 2, 2), got {tuple(f.shape)}")
+    ft = f.reshape(-1, head_dim // 2 * 4)
+    if ft.shape[0] not in (1, m):
+        raise ValueError(f"freqs_cis holds {ft.shape[0]} token rows for {m} tokens")
+    ft = ft.contiguous()
+    fstride = 0 if ft.shape[0] == 1 else ft.stride(0)
+    if inplace:
+        qo, ko = q2, k2
+    else:
+        qo = torch.empty(m, width, dtype=q.dtype, device=q.device)
+        ko = None if k2 is None else torch.empty(m, width, dtype=q.dtype, device=q.device)
+    if m:
+        call("xmh3_norm_rope", q2.data_ptr(), qo.data_ptr(), ptr(k2), ptr(ko), DTYPE_CODE[q.dtype], m, width,
+             ldq, qo.stride(0), sc.data_ptr(), sh.data_ptr(), DTYPE_CODE[sc.dtype], sc.stride(0), g1,
+             ft.data_ptr(), DTYPE_CODE[ft.dtype], fstride, head_dim, float(eps), stream_of(q))
+    if inplace:
+        if q2.data_ptr() != q.data_ptr():
+            q.copy_(q2.reshape(q.shape))
+        if k is not None and k2.data_ptr() != k.data_ptr():
+            k.copy_(k2.reshape(k.shape))
+        return q, k
+    return qo.reshape(q.shape), (None if ko is None else ko.reshape(k.shape))
+
+
+# --------------------------------------------------------------------------- in-place checks
+
+def _storage_span(x: torch.Tensor) -> tuple[int, int]:
+    lo = hi = x.storage_offset()
+    for size, stride in zip(x.shape, x.stride()):
+        ext = (size - 1) * stride
+        lo += min(0, ext)
+        hi += max(0, ext)
+    es = x.element_size()
+    return lo * es, (hi + 1) * es - 1
+
+
+def _may_overlap(x: torch.Tensor, y: torch.Tensor) -> bool:
+    if x.numel() == 0 or y.numel() == 0 or x.device != y.device:
+        return False
+    if x.untyped_storage().data_ptr() != y.untyped_storage().data_ptr():
+        return False
+    a0, a1 = _storage_span(x)
+    b0, b1 = _storage_span(y)
+    if max(a0, b0) > min(a1, b1):
+        return False
+    # same-layout strided views interleaved inside one period (packed QKV)
+    if x.shape == y.shape and x.stride() == y.stride() and x.stride()[-1] == 1:
+        extent, i = 1, x.dim()
+        while i > 0 and x.stride(i - 1) == extent:
+            extent *= x.shape[i - 1]
+            i -= 1
+        outer = [s for sz, s in zip(x.shape[:i], x.stride()[:i]) if sz > 1]
+        if outer:
+            period = min(outer)
+            if period > 0 and all(s % period == 0 for s in outer):
+                delta = abs(x.storage_offset() - y.storage_offset())
+                if delta >= extent and delta + extent <= period:
+                    return False
+    return True
+
+
+def check_rope_inplace(*xs: torch.Tensor, readonly: tuple = ()) -> None:
+    """The in-place guards of CK/_rope_utils.py:91-123: no autograd, no
+    self-overlapping views, no overlap between q and k or with the table and
+    scales (same error types and messages)."""
+    for t in (*xs, *readonly):
+        if t is not None and t.requires_grad:
+            raise RuntimeError("in-place RoPE operations are inference-only and do not support autograd")
+    for x in xs:
+        need = 1
+        for stride, size in sorted((abs(st), sz) for sz, st in zip(x.shape, x.stride()) if sz > 1):
+            if stride < need:
+                raise ValueError("in-place RoPE requires views without internal overlap")
+            need = stride * size
+    if len(xs) == 2 and _may_overlap(xs[0], xs[1]):
+        raise ValueError("paired in-place RoPE requires non-overlapping input storage")
+    for x in xs:
+        for src in readonly:
+            if src is not None and _may_overlap(x, src):
+                raise ValueError("in-place RoPE inputs must not overlap frequencies or scales")
+
+
+# --------------------------------------------------------------------------- registration
+
+def _k_rule(kw) -> ValidationResult:
+    x, w = kw.get("x"), kw.get("weight")
+    if x is not None and w is not None and x.device != w.device and w.device.type != "cpu":
+        return ValidationResult.fail("weight", "weight on a different device")
+    return ValidationResult.ok()
+
+
+def _capabilities() -> dict[str, FunctionConstraints]:
+    on_gpu = frozenset({"cuda"})
+    return {
+        "quantize_int8_rowwise": FunctionConstraints(
+            params={"x": ParamConstraint(dtypes=FLOATS, shape_rules=(MinDims(1),))}, default_devices=on_gpu),
+        "int8_linear": FunctionConstraints(
+            params={"x": ParamConstraint(dtypes=FLOATS),
+                    "weight": ParamConstraint(dtypes=frozenset({torch.int8}), devices=frozenset({"cuda", "cpu"}),
+                                              shape_rules=(ExactDims(2),)),
+                    "weight_scale": ParamConstraint(dtypes=FLOATS, devices=frozenset({"cuda", "cpu"})),
+                    "bias": ParamConstraint(dtypes=FLOATS, devices=frozenset({"cuda", "cpu"}))},
+            default_devices=on_gpu, call_rules=(_k_rule,)),
+        "w4a8_int8_linear": FunctionConstraints(
+            params={"x": ParamConstraint(dtypes=FLOATS),
+                    "qdata": ParamConstraint(dtypes=frozenset({torch.int8}), shape_rules=(ExactDims(2),))},
+            default_devices=on_gpu),
+        "dequant_int4_grouped_to_int8": FunctionConstraints(
+            params={"qdata": ParamConstraint(dtypes=frozenset({torch.int8}), shape_rules=(ExactDims(2),))},
+            default_devices=on_gpu),
+        "w8a8_mlp": FunctionConstraints(
+            params={"x": ParamConstraint(dtypes=FLOATS),
+                    "w1": ParamConstraint(dtypes=frozenset({torch.int8}), shape_rules=(ExactDims(2),)),
+                    "w2": ParamConstraint(dtypes=frozenset({torch.int8}), shape_rules=(ExactDims(2),))},
+            default_devices=on_gpu),
+        "w4a8_mlp": FunctionConstraints(
+            params={"x": ParamConstraint(dtypes=FLOATS)}, default_devices=on_gpu),
+        "rms_adaln": FunctionConstraints(
+            params={"x": ParamConstraint(dtypes=FLOATS), "scale": ParamConstraint(dtypes=FLOATS),
+                    "shift": ParamConstraint(dtypes=FLOATS)}, default_devices=on_gpu),
+        "norm_rope": FunctionConstraints(
+            params={"q": ParamConstraint(dtypes=HALFS), "k": ParamConstraint(dtypes=HALFS)},
+            default_devices=on_gpu),
+        **{name: FunctionConstraints(params={p: ParamConstraint(dtypes=FLOATS) for p in ps},
+                                     default_devices=on_gpu)
+           for name, ps in {
+               "apply_rope_split_half": ("xq", "xk"), "apply_rope_split_half_": ("xq", "xk"),
+               "apply_rope_split_half1": ("x",), "apply_rope_split_half1_": ("x",),
+               "rms_rope_split_half": ("q", "k"), "rms_rope_split_half_": ("q", "k"),
+               "rms_rope_split_half1": ("x",), "rms_rope_split_half1_": ("x",)}.items()},
+    }
+
+
+def register() -> None:
+    import sys
+    registry.register("mi355x", sys.modules[__name__], _capabilities())
+
+
+register()

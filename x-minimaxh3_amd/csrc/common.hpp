@@ -1,0 +1,111 @@
+// Shared device/host helpers for the gfx950 kernels of the quantized
+// DiT-block path. Everything here is written for CDNA4 (wave64, MFMA, LDS);
+// there is no CUDA or multi-target code.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace xmh3 {
+
+// dtype codes of the reference's op boundary
+// (CK/backends/eager/quantization.py:34-42): 0 fp32, 1 fp16, 2 bf16.
+enum DtypeCode : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+// input-activation codes (CK/backends/_activations.py:19-24).
+enum ActCode : int { ACT_NONE = 0, ACT_GELU_TANH = 1, ACT_SWIGLU = 2 };
+
+// status codes returned by every extern "C" entry point
+enum Status : int { XMH3_OK = 0, XMH3_EINVAL = 1, XMH3_EHIP = 2, XMH3_EUNSUPPORTED = 3 };
+
+// ---------------------------------------------------------------------------
+// scalar conversions (bit exact; fp32 -> bf16 rounds to nearest even)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)v;
+}
+__device__ __forceinline__ uint32_t f32_to_f16(float f) {
+  _Float16 v = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
+  return (uint32_t)__builtin_bit_cast(uint16_t, v);
+}
+
+// Element-type traits: storage type, fp32 view and rounding back to T.
+struct BF16T {
+  using storage = uint16_t;
+  static constexpr int code = DT_BF16;
+  __device__ static float load(uint32_t b) { return bf16_to_f32(b); }
+  __device__ static uint32_t store(float f) { return f32_to_bf16(f); }
+  __device__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+  __device__ static float tiny() { return 1.17549435e-38f; }
+};
+struct F16T {
+  using storage = uint16_t;
+  static constexpr int code = DT_F16;
+  __device__ static float load(uint32_t b) { return f16_to_f32(b); }
+  __device__ static uint32_t store(float f) { return f32_to_f16(f); }
+  __device__ static float round(float f) { return f16_to_f32(f32_to_f16(f)); }
+  __device__ static float tiny() { return 6.103515625e-05f; }
+};
+struct F32T {
+  using storage = float;
+  static constexpr int code = DT_F32;
+  __device__ static float load(float f) { return f; }
+  __device__ static float store(float f) { return f; }
+  __device__ static float round(float f) { return f; }
+  __device__ static float tiny() { return 1.17549435e-38f; }
+};
+
+// ---------------------------------------------------------------------------
+// wave64 reductions
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// GELU with the tanh approximation, 0.5*h*(1+tanh(u)),
+// u = sqrt(2/pi)*(h + 0.044715*h^3), evaluated as h / (1 + exp(-2u)) (the
+// same function; no cancellation as tanh(u) -> -1). Constants from the
+// published formula.
+__device__ __forceinline__ float gelu_tanh_f32(float h) {
+  const float kBeta = 0.7978845608028654f;   // sqrt(2/pi)
+  const float kKappa = 0.044715f;
+  float cube = h * h * h;
+  float u = kBeta * (h + kKappa * cube);
+  // exp(-2u) = 2^(-2u*log2(e))
+  float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);
+  return h * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
+// ---------------------------------------------------------------------------
+// host-side error plumbing (no C++ exception crosses the C ABI)
+// ---------------------------------------------------------------------------
+void set_last_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int check_launch(const char* what);
+
+}  // namespace xmh3
+
+#define XMH3_REQUIRE(cond, msg)                                    \
+  do {                                                             \
+    if (!(cond)) return ::xmh3::fail(::xmh3::XMH3_EINVAL, (msg));  \
+  } while (0)

@@ -1,0 +1,325 @@
+// int8 x int8 -> int32 GEMM on gfx950 MFMA with fused epilogues.
+//
+//   acc[m,n] = sum_k A[m,k] * B[n,k]        (A: [M,K] row-major activations,
+//                                             B: [N,K] row-major weights)
+// Epilogues (the reference's dequant, CK/backends/eager/quantization.py:1028-1054,
+// CK = backends/turbo/vendor/comfy_kitchen):
+//   EPI_DEQUANT : out = T(float(acc) * (sx[m] * sw[n])) (+ bias in T)
+//   EPI_GELU    : h = bf16(...as above...); g = bf16(gelu_tanh(h)); store g and
+//                 atomically fold max|g| per row into row_amax (fp32 bits) --
+//                 fc1 of the fused MLP, feeding the per-token requant of fc2
+//   EPI_INT32   : raw int32 accumulators (parity of the contraction itself)
+//
+// Tiling: 256x256 block tile, 4 waves in a 2x2 grid, each wave owning a
+// 128x128 sub-tile held as 8x8 accumulators of v_mfma_i32_16x16x64_i8 (256
+// AGPRs). K advances BK bytes per step; A and B tiles are staged through LDS
+// (double buffered, XOR-swizzled 16-byte chunks so ds_read_b128 is
+// conflict-free), with the next step's global loads in flight while the
+// current step's MFMAs run. Workgroups are remapped so each XCD (own L2)
+// walks a contiguous, GROUP_M-swizzled band of tiles.
+#include "common.hpp"
+
+namespace xmh3 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+enum Epi : int { EPI_DEQUANT = 0, EPI_GELU = 1, EPI_INT32 = 2 };
+
+struct GemmArgs {
+  const int8_t* A;
+  const int8_t* B;
+  int64_t lda, ldb;  // bytes
+  int M, N, K;
+  const float* sx;   // [M]
+  const float* sw;   // [N] or [1]
+  int sw_per_channel;
+  const void* bias;  // [N] in the output dtype, nullable
+  void* out;
+  int64_t ldo;       // elements
+  uint32_t* row_amax;
+  int tiles_m, tiles_n;
+};
+
+constexpr int BM = 256, BN = 256, NTHREADS = 256;
+constexpr int GROUP_M = 8;
+constexpr int NUM_XCD = 8;
+
+// XOR swizzle of the 16-byte chunk index inside an LDS row of BK bytes.
+template <int BK>
+__device__ __forceinline__ int swz(int row, int chunk) {
+  if constexpr (BK == 64) return chunk ^ ((row >> 1) & 3);
+  else return chunk ^ (row & 7);
+}
+
+// Map the hardware workgroup id to (tile_m, tile_n): contiguous logical tile
+// ranges per XCD (workgroups are dealt round-robin over the XCDs), then a
+// GROUP_M swizzle inside the logical order.
+__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int q = total / NUM_XCD, r = total % NUM_XCD;
+  const int x = pid % NUM_XCD, j = pid / NUM_XCD;
+  const int logical = (x < r) ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
+  const int in_group = GROUP_M * tiles_n;
+  const int group = logical / in_group;
+  const int first_m = group * GROUP_M;
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int rem = logical - group * in_group;
+  tm = first_m + rem % gsize;
+  tn = rem / gsize;
+}
+
+// 4 consecutive outputs -> one 8- or 16-byte store
+__device__ __forceinline__ void store4(uint16_t* p, const float* v, BF16T) {
+  uint2 w;
+  w.x = f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16);
+  w.y = f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16);
+  *reinterpret_cast<uint2*>(p) = w;
+}
+__device__ __forceinline__ void store4(uint16_t* p, const float* v, F16T) {
+  uint2 w;
+  w.x = f32_to_f16(v[0]) | (f32_to_f16(v[1]) << 16);
+  w.y = f32_to_f16(v[2]) | (f32_to_f16(v[3]) << 16);
+  *reinterpret_cast<uint2*>(p) = w;
+}
+__device__ __forceinline__ void store4(float* p, const float* v, F32T) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+template <int BK, int EPI, typename TO, bool VEC_OUT>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_kernel(GemmArgs p) {
+  constexpr int CPR = BK / 16;                 // 16-byte chunks per tile row
+  constexpr int TILE_BYTES = BM * BK;          // A tile == B tile size
+  constexpr int LOADS = TILE_BYTES / 16 / NTHREADS;  // 16-byte loads per thread per operand
+  constexpr int KSUB = BK / 64;                // MFMA k-steps per BK
+  __shared__ __attribute__((aligned(16))) int8_t lds[2][2][TILE_BYTES];
+
+  int tm, tn;
+  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // global load coordinates (same for A and B)
+  int ld_row[LOADS], ld_chunk[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int c = tid + NTHREADS * i;
+    ld_row[i] = c / CPR;
+    ld_chunk[i] = c % CPR;
+  }
+  const int8_t* a_ptr[LOADS];
+  const int8_t* b_ptr[LOADS];
+  bool a_ok[LOADS], b_ok[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) {
+    const int ar = m0 + ld_row[i], br = n0 + ld_row[i];
+    a_ok[i] = ar < p.M;
+    b_ok[i] = br < p.N;
+    a_ptr[i] = p.A + (int64_t)(a_ok[i] ? ar : 0) * p.lda + ld_chunk[i] * 16;
+    b_ptr[i] = p.B + (int64_t)(b_ok[i] ? br : 0) * p.ldb + ld_chunk[i] * 16;
+  }
+  int lds_off[LOADS];
+#pragma unroll
+  for (int i = 0; i < LOADS; ++i) lds_off[i] = ld_row[i] * BK + swz<BK>(ld_row[i], ld_chunk[i]) * 16;
+
+  uint4 ra[LOADS], rb[LOADS];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      const bool kok = (k0 + ld_chunk[i] * 16) < p.K;
+      ra[i] = (a_ok[i] && kok) ? *reinterpret_cast<const uint4*>(a_ptr[i] + k0) : make_uint4(0, 0, 0, 0);
+      rb[i] = (b_ok[i] && kok) ? *reinterpret_cast<const uint4*>(b_ptr[i] + k0) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      *reinterpret_cast<uint4*>(&lds[buf][0][lds_off[i]]) = ra[i];
+      *reinterpret_cast<uint4*>(&lds[buf][1][lds_off[i]]) = rb[i];
+    }
+  };
+
+  v4i acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  // fragment read offsets: row = base + lane%16, chunk = kk*4 + lane/16
+  const int frow = lane & 15, fchunk = lane >> 4;
+
+  const int ksteps = (p.K + BK - 1) / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < ksteps; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < ksteps) gload((kt + 1) * BK);
+#pragma unroll
+    for (int kk = 0; kk < KSUB; ++kk) {
+      v4i af[8], bf[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = wm * 128 + i * 16 + frow;
+        af[i] = *reinterpret_cast<const v4i*>(&lds[cur][0][r * BK + swz<BK>(r, kk * 4 + fchunk) * 16]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = wn * 128 + j * 16 + frow;
+        bf[j] = *reinterpret_cast<const v4i*>(&lds[cur][1][r * BK + swz<BK>(r, kk * 4 + fchunk) * 16]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < ksteps) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  // lane holds, for block (i, j): row m = base_m + i*16 + lane%16,
+  // columns n = base_n + j*16 + 4*(lane/16) + {0..3}.
+  const int em = m0 + wm * 128 + (lane & 15);
+  const int en = n0 + wn * 128 + 4 * (lane >> 4);
+  float amax_row[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax_row[i] = 0.0f;
+
+  float swv[8][4];
+  if constexpr (EPI != EPI_INT32) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = en + j * 16 + r;
+        swv[j][r] = p.sw_per_channel ? (n < p.N ? p.sw[n] : 0.0f) : p.sw[0];
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int m = em + i * 16;
+    if (m >= p.M) continue;
+    if constexpr (EPI == EPI_INT32) {
+      int32_t* orow = static_cast<int32_t*>(p.out) + (int64_t)m * p.ldo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = en + j * 16;
+        if (VEC_OUT && n + 3 < p.N) {
+          *reinterpret_cast<v4i*>(orow + n) = acc[i][j];
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.N) orow[n + r] = acc[i][j][r];
+        }
+      }
+    } else {
+      const float sxm = p.sx[m];
+      typename TO::storage* orow = static_cast<typename TO::storage*>(p.out) + (int64_t)m * p.ldo;
+      const typename TO::storage* brow = static_cast<const typename TO::storage*>(p.bias);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = en + j * 16;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float scl = sxm * swv[j][r];
+          float y = TO::round((float)acc[i][j][r] * scl);
+          if (brow && n + r < p.N) y = TO::round(y + TO::load(brow[n + r]));
+          if constexpr (EPI == EPI_GELU) {
+            y = TO::round(gelu_tanh_f32(y));
+            if (n + r < p.N) amax_row[i] = fmaxf(amax_row[i], fabsf(y));
+          }
+          v[r] = y;
+        }
+        if (VEC_OUT && n + 3 < p.N) {
+          store4(orow + n, v, TO{});
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.N) orow[n + r] = (typename TO::storage)TO::store(v[r]);
+        }
+      }
+    }
+  }
+  if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float a = amax_row[i];
+      a = fmaxf(a, __shfl_xor(a, 16, 64));
+      a = fmaxf(a, __shfl_xor(a, 32, 64));
+      const int m = em + i * 16;
+      if (lane < 16 && m < p.M) atomicMax(p.row_amax + m, __float_as_uint(a));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host launcher
+// ---------------------------------------------------------------------------
+template <int BK, int EPI, typename TO>
+static int launch_gemm_T(GemmArgs& a, bool vec, hipStream_t st) {
+  dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  if (vec)
+    hipLaunchKernelGGL((gemm_i8_kernel<BK, EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_i8_kernel<BK, EPI, TO, false>), grid, dim3(NTHREADS), 0, st, a);
+  return check_launch("gemm_i8_kernel");
+}
+
+int int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_t M, int64_t N,
+              int64_t K, const float* sx, const float* sw, int sw_per_channel, const void* bias,
+              void* out, int out_dtype, int64_t ldo, int epilogue, uint32_t* row_amax,
+              hipStream_t st) {
+  XMH3_REQUIRE(M >= 0 && N >= 0 && K >= 0, "int8_gemm: negative size");
+  XMH3_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "int8_gemm: size too large");
+  if (M == 0 || N == 0) return XMH3_OK;
+  XMH3_REQUIRE(A && B && out, "int8_gemm: null operand");
+  XMH3_REQUIRE(K % 16 == 0, "int8_gemm: K must be a multiple of 16");
+  XMH3_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && lda >= K && ldb >= K,
+               "int8_gemm: row strides must be multiples of 16 bytes and >= K");
+  XMH3_REQUIRE((uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0, "int8_gemm: operands must be 16-byte aligned");
+  XMH3_REQUIRE(ldo >= N, "int8_gemm: output stride < N");
+  XMH3_REQUIRE(K <= 131072, "int8_gemm: K > 131072 could overflow int32 accumulators");
+  if (epilogue != EPI_INT32) XMH3_REQUIRE(sx && sw, "int8_gemm: scales required");
+  if (epilogue == EPI_GELU) {
+    XMH3_REQUIRE(row_amax, "int8_gemm: gelu epilogue needs row_amax");
+    XMH3_REQUIRE(out_dtype == DT_BF16, "int8_gemm: gelu epilogue writes bf16");
+  }
+  GemmArgs a;
+  a.A = A; a.B = B; a.lda = lda; a.ldb = ldb;
+  a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.sx = sx; a.sw = sw; a.sw_per_channel = sw_per_channel;
+  a.bias = bias; a.out = out; a.ldo = ldo; a.row_amax = row_amax;
+  a.tiles_m = (int)((M + BM - 1) / BM);
+  a.tiles_n = (int)((N + BN - 1) / BN);
+  XMH3_REQUIRE((int64_t)a.tiles_m * a.tiles_n < (1LL << 31), "int8_gemm: grid too large");
+  const int esize = (epilogue == EPI_INT32 || out_dtype == DT_F32) ? 4 : 2;
+  const bool vec = (ldo % 4 == 0) && ((uintptr_t)out % (4 * esize) == 0);
+  // BK=128 needs 128 KiB of LDS (2 stages x 2 operands x 32 KiB)
+  switch (epilogue) {
+    case EPI_INT32:
+      return launch_gemm_T<128, EPI_INT32, F32T>(a, vec, st);
+    case EPI_GELU:
+      return launch_gemm_T<128, EPI_GELU, BF16T>(a, vec, st);
+    case EPI_DEQUANT:
+      if (out_dtype == DT_BF16) return launch_gemm_T<128, EPI_DEQUANT, BF16T>(a, vec, st);
+      if (out_dtype == DT_F16) return launch_gemm_T<128, EPI_DEQUANT, F16T>(a, vec, st);
+      if (out_dtype == DT_F32) return launch_gemm_T<128, EPI_DEQUANT, F32T>(a, vec, st);
+      return fail(XMH3_EUNSUPPORTED, "int8_gemm: out dtype must be fp32, fp16 or bf16");
+    default:
+      return fail(XMH3_EINVAL, "int8_gemm: unknown epilogue");
+  }
+}
+
+}  // namespace xmh3
+
+extern "C" int xmh3_int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_t M,
+                              int64_t N, int64_t K, const float* sx, const float* sw,
+                              int sw_per_channel, const void* bias, void* out, int out_dtype,
+                              int64_t ldo, int epilogue, uint32_t* row_absmax_bits,
+                              hipStream_t stream) {
+  return xmh3::int8_gemm(A, lda, B, ldb, M, N, K, sx, sw, sw_per_channel, bias, out, out_dtype, ldo,
+                         epilogue, row_absmax_bits, stream);
+}

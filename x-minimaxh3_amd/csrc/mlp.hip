@@ -1,0 +1,126 @@
+// The W8A8 / W4A8 MLP block  y = fc2(gelu_tanh(fc1(x)))  on one stream.
+//
+// Reference op chain (CK = backends/turbo/vendor/comfy_kitchen):
+//   h = int8_linear(x, W1, s1)                      CK/backends/eager/quantization.py:971-1056
+//   y = int8_linear(h, W2, s2, input_act="gelu_tanh")
+// Kernel chain here (four launches, all on the caller's stream):
+//   1. per-token quant of x -> q1, sx           (also clears the row-amax slots)
+//   2. int8 GEMM q1 x W1^T, epilogue: dequant -> bf16 h -> bf16 gelu(h) = g,
+//      store g, fold max|g| per row into row_amax
+//   3. streaming requant of g with the finished row amax -> q2, sg
+//   4. int8 GEMM q2 x W2^T, epilogue: dequant -> y
+// The W4A8 variant first turns both packed int4 weights into the int8 grid.
+// Workspace (caller-owned, 256-byte aligned segments):
+//   q1 [M,D] i8 | sx [M] f32 | g [M,F] bf16 | amax [M] u32 | q2 [M,F] i8 | sg [M] f32
+//   (+ W1 [F,D] i8 | W2 [D,F] i8 for W4A8)
+#include "common.hpp"
+
+namespace xmh3 {
+
+int quantize_rows(const void* x, int x_dtype, int input_act, int64_t M, int64_t K, int64_t ldx,
+                  int8_t* q, int64_t ldq, float* scale, uint32_t* zero_rows, hipStream_t st);
+int requant_rows(const void* g, int g_dtype, int64_t M, int64_t K, int64_t ldg,
+                 const uint32_t* row_amax, int8_t* q, int64_t ldq, float* scale, hipStream_t st);
+int int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_t M, int64_t N,
+              int64_t K, const float* sx, const float* sw, int sw_per_channel, const void* bias,
+              void* out, int out_dtype, int64_t ldo, int epilogue, uint32_t* row_amax,
+              hipStream_t st);
+int w4_decode(const uint8_t* packed, const void* s_rel, int s_rel_dtype, const float* codebook,
+              int64_t N, int64_t K, int64_t G, int8_t* out, hipStream_t st);
+
+static inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+struct MlpWs {
+  int8_t* q1; float* sx; uint16_t* g; uint32_t* amax; int8_t* q2; float* sg;
+  int8_t* w1; int8_t* w2;
+  size_t bytes;
+};
+
+static MlpWs carve(void* base, int64_t M, int64_t D, int64_t F, bool w4) {
+  MlpWs w{};
+  size_t off = 0;
+  auto take = [&](size_t n) { size_t o = off; off = align256(off + n); return o; };
+  const size_t o_q1 = take((size_t)M * D), o_sx = take((size_t)M * 4), o_g = take((size_t)M * F * 2),
+               o_am = take((size_t)M * 4), o_q2 = take((size_t)M * F), o_sg = take((size_t)M * 4);
+  size_t o_w1 = 0, o_w2 = 0;
+  if (w4) { o_w1 = take((size_t)F * D); o_w2 = take((size_t)D * F); }
+  w.bytes = off;
+  char* b = static_cast<char*>(base);
+  if (b) {
+    w.q1 = reinterpret_cast<int8_t*>(b + o_q1);
+    w.sx = reinterpret_cast<float*>(b + o_sx);
+    w.g = reinterpret_cast<uint16_t*>(b + o_g);
+    w.amax = reinterpret_cast<uint32_t*>(b + o_am);
+    w.q2 = reinterpret_cast<int8_t*>(b + o_q2);
+    w.sg = reinterpret_cast<float*>(b + o_sg);
+    if (w4) { w.w1 = reinterpret_cast<int8_t*>(b + o_w1); w.w2 = reinterpret_cast<int8_t*>(b + o_w2); }
+  }
+  return w;
+}
+
+static int mlp_core(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                    const int8_t* w1, const float* s1, int s1_pc, const int8_t* w2, const float* s2,
+                    int s2_pc, void* y, int64_t ldy, const MlpWs& ws, hipStream_t st) {
+  int rc = quantize_rows(x, x_dtype, ACT_NONE, M, D, ldx, ws.q1, D, ws.sx, ws.amax, st);
+  if (rc) return rc;
+  rc = int8_gemm(ws.q1, D, w1, D, M, F, D, ws.sx, s1, s1_pc, nullptr, ws.g, DT_BF16, F, 1 /*gelu*/,
+                 ws.amax, st);
+  if (rc) return rc;
+  rc = requant_rows(ws.g, DT_BF16, M, F, F, ws.amax, ws.q2, F, ws.sg, st);
+  if (rc) return rc;
+  return int8_gemm(ws.q2, F, w2, F, M, D, F, ws.sg, s2, s2_pc, nullptr, y, DT_BF16, ldy,
+                   0 /*dequant*/, nullptr, st);
+}
+
+static int check_mlp_shapes(int64_t M, int64_t D, int64_t F, int64_t ldx, int64_t ldy) {
+  XMH3_REQUIRE(M >= 0 && D > 0 && F > 0, "mlp: bad sizes");
+  XMH3_REQUIRE(D % 16 == 0 && F % 16 == 0, "mlp: d_model and ffn must be multiples of 16");
+  XMH3_REQUIRE(ldx >= D && ldy >= D && ldx % 8 == 0, "mlp: bad strides");
+  return XMH3_OK;
+}
+
+}  // namespace xmh3
+
+using namespace xmh3;
+
+extern "C" size_t xmh3_w8a8_mlp_workspace_bytes(int64_t M, int64_t D, int64_t F) {
+  return carve(nullptr, M, D, F, false).bytes;
+}
+
+extern "C" size_t xmh3_w4a8_mlp_workspace_bytes(int64_t M, int64_t D, int64_t F) {
+  return carve(nullptr, M, D, F, true).bytes;
+}
+
+extern "C" int xmh3_w8a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                             const int8_t* w1, const float* s1, int s1_per_channel, const int8_t* w2,
+                             const float* s2, int s2_per_channel, void* y, int64_t ldy,
+                             void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int rc = check_mlp_shapes(M, D, F, ldx, ldy);
+  if (rc) return rc;
+  if (M == 0) return XMH3_OK;
+  MlpWs ws = carve(workspace, M, D, F, false);
+  XMH3_REQUIRE(workspace && workspace_bytes >= ws.bytes, "w8a8_mlp: workspace too small");
+  XMH3_REQUIRE(x && w1 && s1 && w2 && s2 && y, "w8a8_mlp: null pointer");
+  return mlp_core(x, x_dtype, M, D, F, ldx, w1, s1, s1_per_channel, w2, s2, s2_per_channel, y, ldy, ws,
+                  stream);
+}
+
+extern "C" int xmh3_w4a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                             const uint8_t* w1_packed, const void* w1_srel, const float* w1_schannel,
+                             const uint8_t* w2_packed, const void* w2_srel, const float* w2_schannel,
+                             int srel_dtype, int64_t group_size, void* y, int64_t ldy,
+                             void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  int rc = check_mlp_shapes(M, D, F, ldx, ldy);
+  if (rc) return rc;
+  if (M == 0) return XMH3_OK;
+  MlpWs ws = carve(workspace, M, D, F, true);
+  XMH3_REQUIRE(workspace && workspace_bytes >= ws.bytes, "w4a8_mlp: workspace too small");
+  XMH3_REQUIRE(x && w1_packed && w1_srel && w1_schannel && w2_packed && w2_srel && w2_schannel && y,
+               "w4a8_mlp: null pointer");
+  rc = w4_decode(w1_packed, w1_srel, srel_dtype, nullptr, F, D, group_size, ws.w1, stream);
+  if (rc) return rc;
+  rc = w4_decode(w2_packed, w2_srel, srel_dtype, nullptr, D, F, group_size, ws.w2, stream);
+  if (rc) return rc;
+  return mlp_core(x, x_dtype, M, D, F, ldx, ws.w1, w1_schannel, 1, ws.w2, w2_schannel, 1, y, ldy, ws,
+                  stream);
+}

@@ -1,0 +1,542 @@
+// Memory-bound normalisation / rotary kernels for gfx950.
+//
+// Row-span family (one wave64 per token row, the row held in VGPRs, 16-byte
+// loads and stores, wave reduction of the sum of squares, no LDS):
+//   * norm_rope  : out = rope_split_half(rms_adaln(x, scale, shift, eps), freqs)
+//                  for Q and K of one token in the same wave (the table row is
+//                  read once for both); RMS over the full row, rotation per
+//                  head. (CK/backends/eager/adaln.py:17-20 then
+//                  CK/backends/eager/rope.py:39-42)
+//   * rms_adaln  : rms_norm(x [* weight]) * (1 + scale[r]) + shift[r] with the
+//                  modulation row r = row_map[token] or token / group
+//                  (CK/backends/eager/adaln.py:17-20,
+//                   h3serve/native_engine/model/kernels.py:7623-7634)
+// Head-span family (a power-of-two group of lanes per (token, head)):
+//   * rms_rope_split_half : per-head rms_norm with weight, split-half rotation
+//                  of the first rot_dim dims, tail norm-only, in place on
+//                  strided [B,S,H,D] (CK/backends/eager/rope.py:67-92,178-189)
+//   * rope_split_half     : the rotation alone (CK/backends/eager/rope.py:39-48)
+//
+// Rounding points follow the eager op order exactly: rms_norm rounds once to
+// x's dtype ((x*rrms)*w in fp32); 1+scale, the product and the sum each round
+// to the promoted dtype; the rotation's two products and their sum round to the
+// table's dtype, then the result rounds to x's dtype. No FMA contraction
+// (-ffp-contract=off); the only fused multiply-add is in the sum of squares.
+// CK = backends/turbo/vendor/comfy_kitchen.
+#include "common.hpp"
+
+#include <type_traits>
+
+namespace xmh3 {
+
+// 8 x 16-bit or 8 x fp32 values as raw storage
+template <typename T> struct V8;
+template <> struct V8<BF16T> { uint4 v; };
+template <> struct V8<F16T> { uint4 v; };
+template <> struct V8<F32T> { uint4 v[2]; };
+
+template <typename T>
+__device__ __forceinline__ void ld8(const void* base, int64_t idx, V8<T>& d) {
+  const typename T::storage* p = static_cast<const typename T::storage*>(base) + idx;
+  if constexpr (sizeof(typename T::storage) == 2) d.v = *reinterpret_cast<const uint4*>(p);
+  else { d.v[0] = *reinterpret_cast<const uint4*>(p); d.v[1] = *reinterpret_cast<const uint4*>(p + 4); }
+}
+template <typename T>
+__device__ __forceinline__ void st8(void* base, int64_t idx, const V8<T>& d) {
+  typename T::storage* p = static_cast<typename T::storage*>(base) + idx;
+  if constexpr (sizeof(typename T::storage) == 2) *reinterpret_cast<uint4*>(p) = d.v;
+  else { *reinterpret_cast<uint4*>(p) = d.v[0]; *reinterpret_cast<uint4*>(p + 4) = d.v[1]; }
+}
+template <typename T>
+__device__ __forceinline__ float g8(const V8<T>& d, int j) {
+  if constexpr (sizeof(typename T::storage) == 2) {
+    uint32_t w = (&d.v.x)[j >> 1];
+    return T::load((j & 1) ? (w >> 16) : (w & 0xffffu));
+  } else {
+    return __uint_as_float((&d.v[j >> 2].x)[j & 3]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void s8(V8<T>& d, int j, float f) {
+  if constexpr (sizeof(typename T::storage) == 2) {
+    uint32_t& w = (&d.v.x)[j >> 1];
+    uint32_t b = T::store(f);
+    w = (j & 1) ? ((w & 0xffffu) | (b << 16)) : ((w & 0xffff0000u) | b);
+  } else {
+    (&d.v[j >> 2].x)[j & 3] = __float_as_uint(f);
+  }
+}
+
+// type promotion of (x dtype, modulation dtype) as torch does for x * (1 + s)
+template <typename TX, typename TM> struct Promote { using type = TX; };
+template <> struct Promote<BF16T, F32T> { using type = F32T; };
+template <> struct Promote<F16T, F32T> { using type = F32T; };
+template <> struct Promote<BF16T, F16T> { using type = F32T; };
+template <> struct Promote<F16T, BF16T> { using type = F32T; };
+
+// one rotated pair in the table dtype TF, result rounded to TO
+template <typename TF, typename TO>
+__device__ __forceinline__ void rotate_pair(float a0, float a1, float f00, float f01, float f10,
+                                            float f11, float& r0, float& r1) {
+  const float x0 = TF::round(a0), x1 = TF::round(a1);  // x.to(freqs.dtype)
+  r0 = TO::round(TF::round(TF::round(f00 * x0) + TF::round(f01 * x1)));
+  r1 = TO::round(TF::round(TF::round(f10 * x0) + TF::round(f11 * x1)));
+}
+
+// table entries for 8 consecutive pairs: [pair][2][2] in TF
+template <typename TF>
+struct Tab8 { float f[8][4]; };
+
+template <typename TF>
+__device__ __forceinline__ void load_tab8(const void* base, int64_t idx, Tab8<TF>& t) {
+  // idx: element index of pair p0's f00; 32 consecutive elements
+  V8<TF> raw[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) ld8<TF>(base, idx + q * 8, raw[q]);
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t.f[p][e] = g8<TF>(raw[(p * 4 + e) >> 3], (p * 4 + e) & 7);
+}
+
+// ---------------------------------------------------------------------------
+// row-span kernel
+// ---------------------------------------------------------------------------
+struct RowArgs {
+  const void* x0; void* o0;       // first tensor (Q, or the only one)
+  const void* x1; void* o1;       // optional second tensor (K), same shape
+  int64_t ldx, ldo, rows, D;
+  const void* weight;             // [D] in TX, nullable
+  const void* scale; const void* shift;  // [R, D] in TM (ADALN)
+  int64_t mod_ld;                 // row stride of scale/shift
+  const int32_t* row_map;         // nullable
+  int64_t mod_group;              // token -> modulation row = token / mod_group
+  const void* freqs;              // ROPE: [rows or 1, head_dim/2, 2, 2] in TF
+  int64_t freqs_row_stride;       // elements; 0 = one table row for all tokens
+  int head_dim;
+  float eps;
+};
+
+// ROPE: items are (8 at head offset i, 8 at i + head_dim/2), IPH per head;
+// otherwise items are 8 consecutive elements. NSTEP steps of 64 items.
+template <typename TX, typename TM, typename TF, bool ROPE, bool ADALN, bool WEIGHT, int IPH, int NSTEP>
+__global__ __launch_bounds__(256) void rowspan_kernel(RowArgs a) {
+  using TO = typename std::conditional<ADALN, typename Promote<TX, TM>::type, TX>::type;
+  constexpr int EPI = ROPE ? 16 : 8;                 // elements per item
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int64_t items = a.D / EPI;
+  const int nt = a.x1 ? 2 : 1;
+
+  // element offsets (within the row) of the item's two 8-groups
+  auto item_off = [&](int64_t u, int64_t& o0, int64_t& o1) {
+    if constexpr (ROPE) {
+      const int64_t head = u / IPH;
+      const int it = (int)(u - head * IPH);
+      o0 = head * a.head_dim + it * 8;
+      o1 = o0 + (a.head_dim >> 1);
+    } else {
+      o0 = u * 8;
+      o1 = 0;
+    }
+  };
+
+  V8<TX> v[2][NSTEP][ROPE ? 2 : 1];
+  float ss[2] = {0.0f, 0.0f};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (t >= nt) break;
+    const void* xb = t ? a.x1 : a.x0;
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+      const int64_t u = (int64_t)s * 64 + lane;
+      if (u < items) {
+        int64_t o0, o1;
+        item_off(u, o0, o1);
+        ld8<TX>(xb, row * a.ldx + o0, v[t][s][0]);
+        if constexpr (ROPE) ld8<TX>(xb, row * a.ldx + o1, v[t][s][1]);
+#pragma unroll
+        for (int h = 0; h < (ROPE ? 2 : 1); ++h)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float f = g8<TX>(v[t][s][h], j);
+            ss[t] = fmaf(f, f, ss[t]);
+          }
+      }
+    }
+  }
+  float rr[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float tot = wave_sum(ss[t]);
+    rr[t] = 1.0f / sqrtf(tot / (float)a.D + a.eps);
+  }
+
+  int64_t mrow = 0;
+  if constexpr (ADALN) mrow = a.row_map ? (int64_t)a.row_map[row] : row / a.mod_group;
+
+  // the table row is the same for every head when IPH divides 64
+  Tab8<TF> tab;
+  const int64_t trow = a.freqs_row_stride ? row * a.freqs_row_stride : 0;
+  bool tab_loaded = false;
+
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const int64_t u = (int64_t)s * 64 + lane;
+    if (u >= items) continue;
+    int64_t o0, o1;
+    item_off(u, o0, o1);
+    if constexpr (ROPE) {
+      if (!tab_loaded || (64 % IPH) != 0) {
+        const int it = (int)(u % IPH);
+        load_tab8<TF>(a.freqs, trow + (int64_t)it * 8 * 4, tab);
+        tab_loaded = true;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < (ROPE ? 2 : 1); ++h) {
+      const int64_t col = h ? o1 : o0;
+      float w8[8], t8[8], sh8[8];
+      if constexpr (WEIGHT) {
+        V8<TX> wv;
+        ld8<TX>(a.weight, col, wv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w8[j] = g8<TX>(wv, j);
+      }
+      if constexpr (ADALN) {
+        V8<TM> sv, hv;
+        ld8<TM>(a.scale, mrow * a.mod_ld + col, sv);
+        ld8<TM>(a.shift, mrow * a.mod_ld + col, hv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          t8[j] = TM::round(1.0f + g8<TM>(sv, j));  // (1 + scale) in scale's dtype
+          sh8[j] = g8<TM>(hv, j);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (t >= nt) break;
+        float y8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float n = g8<TX>(v[t][s][h], j) * rr[t];
+          if constexpr (WEIGHT) n = n * w8[j];
+          n = TX::round(n);                           // rms_norm output in x's dtype
+          if constexpr (ADALN) {
+            n = TO::round(n * t8[j]);
+            n = TO::round(n + sh8[j]);
+          }
+          y8[j] = n;
+        }
+        if constexpr (ROPE) {
+          // the rotation needs both halves of the item: stage the modulated
+          // values in the row buffer (exact: the host enforces TO == TX here)
+          static_assert(!ROPE || std::is_same<TO, TX>::value, "rope path keeps x's dtype");
+#pragma unroll
+          for (int j = 0; j < 8; ++j) s8<TX>(v[t][s][h], j, y8[j]);
+        } else {
+          V8<TO> ov;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) s8<TO>(ov, j, y8[j]);
+          st8<TO>(t ? a.o1 : a.o0, row * a.ldo + col, ov);
+        }
+      }
+    }
+    if constexpr (ROPE) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        if (t >= nt) break;
+        V8<TX> r0, r1;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float y0, y1;
+          rotate_pair<TF, TX>(g8<TX>(v[t][s][0], j), g8<TX>(v[t][s][1], j), tab.f[j][0],
+                              tab.f[j][1], tab.f[j][2], tab.f[j][3], y0, y1);
+          s8<TX>(r0, j, y0);
+          s8<TX>(r1, j, y1);
+        }
+        st8<TX>(t ? a.o1 : a.o0, row * a.ldo + o0, r0);
+        st8<TX>(t ? a.o1 : a.o0, row * a.ldo + o1, r1);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// head-span kernel: LPH lanes per (b, s, h) head
+// ---------------------------------------------------------------------------
+struct HeadArgs {
+  void* x; void* out;                 // out may alias x (in place)
+  int64_t B, S, H, D;
+  int64_t sb, ss, sh;                 // element strides of x
+  int64_t ob, os, oh;                 // element strides of out
+  const void* weight;                 // [D] (NORM)
+  const void* freqs;
+  int64_t fb, fs, fh;                 // table strides (0 = broadcast), pairs contiguous
+  int rot;                            // rotated prefix
+  float eps;
+};
+
+template <typename TX, typename TW, typename TF, bool NORM, int LPH>
+__global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t head = (int64_t)blockIdx.x * (256 / LPH) + threadIdx.x / LPH;
+  const int it = threadIdx.x % LPH;
+  const int64_t nheads = a.B * a.S * a.H;
+  // keep whole-group participation in the shuffles: out-of-range groups
+  // compute on a clamped head and skip the stores
+  const bool live = head < nheads;
+  const int64_t hd = live ? head : 0;
+  const int64_t h = hd % a.H, bs = hd / a.H, s = bs % a.S, b = bs / a.S;
+  const int half = a.rot >> 1;
+  const int pair_items = half / 8;
+  const int tail_items = (int)((a.D - a.rot) / 8);
+  const bool is_pair = it < pair_items;
+  const bool is_tail = !is_pair && it < pair_items + tail_items;
+  int64_t c0 = 0, c1 = 0;
+  if (is_pair) { c0 = it * 8; c1 = c0 + half; }
+  else if (is_tail) { c0 = a.rot + (int64_t)(it - pair_items) * 8; }
+  const int64_t xoff = b * a.sb + s * a.ss + h * a.sh;
+  const int64_t ooff = b * a.ob + s * a.os + h * a.oh;
+
+  V8<TX> v0, v1;
+  float ss = 0.0f;
+  if (is_pair || is_tail) {
+    ld8<TX>(a.x, xoff + c0, v0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { const float f = g8<TX>(v0, j); ss = fmaf(f, f, ss); }
+    if (is_pair) {
+      ld8<TX>(a.x, xoff + c1, v1);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) { const float f = g8<TX>(v1, j); ss = fmaf(f, f, ss); }
+    }
+  }
+  float rr = 1.0f;
+  if constexpr (NORM) {
+#pragma unroll
+    for (int o = 1; o < LPH; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    rr = 1.0f / sqrtf(ss / (float)a.D + a.eps);
+  }
+  if (!live || !(is_pair || is_tail)) return;
+
+  auto normalise = [&](V8<TX>& vv, int64_t col) {
+    if constexpr (NORM) {
+      V8<TW> wv;
+      ld8<TW>(a.weight, col, wv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s8<TX>(vv, j, TX::round((g8<TX>(vv, j) * rr) * g8<TW>(wv, j)));
+    }
+  };
+  normalise(v0, c0);
+  if (is_pair) {
+    normalise(v1, c1);
+    Tab8<TF> tab;
+    load_tab8<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 8 * 4, tab);
+    V8<TX> r0, r1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y0, y1;
+      rotate_pair<TF, TX>(g8<TX>(v0, j), g8<TX>(v1, j), tab.f[j][0], tab.f[j][1], tab.f[j][2],
+                          tab.f[j][3], y0, y1);
+      s8<TX>(r0, j, y0);
+      s8<TX>(r1, j, y1);
+    }
+    st8<TX>(a.out, ooff + c0, r0);
+    st8<TX>(a.out, ooff + c1, r1);
+  } else {
+    st8<TX>(a.out, ooff + c0, v0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+template <typename TX, typename TM, typename TF, bool ROPE, bool ADALN, bool WEIGHT, int IPH>
+static int launch_row(RowArgs& a, hipStream_t st) {
+  const int64_t items = a.D / (ROPE ? 16 : 8);
+  const int64_t steps = (items + 63) / 64;
+  dim3 grid((unsigned)((a.rows + 3) / 4));
+#define XMH3_R(N)                                                                                  \
+  if (steps <= N) {                                                                                \
+    hipLaunchKernelGGL((rowspan_kernel<TX, TM, TF, ROPE, ADALN, WEIGHT, IPH, N>), grid, dim3(256), \
+                       0, st, a);                                                                  \
+    return check_launch("rowspan_kernel");                                                         \
+  }
+  if constexpr (ROPE) {
+    XMH3_R(1) XMH3_R(2) XMH3_R(3) XMH3_R(4) XMH3_R(5) XMH3_R(6) XMH3_R(8)
+  } else {
+    XMH3_R(1) XMH3_R(2) XMH3_R(4) XMH3_R(6) XMH3_R(8) XMH3_R(10) XMH3_R(11) XMH3_R(12) XMH3_R(16)
+  }
+#undef XMH3_R
+  return fail(XMH3_EUNSUPPORTED, "row-span kernel: row too wide for the register path");
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+int norm_rope_rows(const void* x0, void* o0, const void* x1, void* o1, int dtype, int64_t rows,
+                   int64_t D, int64_t ldx, int64_t ldo, const void* scale, const void* shift,
+                   int mod_dtype, int64_t mod_ld, int64_t mod_group, const void* freqs,
+                   int freqs_dtype, int64_t freqs_row_stride, int head_dim, float eps,
+                   hipStream_t st) {
+  XMH3_REQUIRE(rows >= 0 && D > 0, "norm_rope: bad sizes");
+  if (rows == 0) return XMH3_OK;
+  XMH3_REQUIRE(x0 && o0 && freqs, "norm_rope: null pointer");
+  XMH3_REQUIRE((x1 == nullptr) == (o1 == nullptr), "norm_rope: second tensor needs both in and out");
+  XMH3_REQUIRE(head_dim == 128 || head_dim == 64 || head_dim == 256,
+               "norm_rope: head_dim must be 64, 128 or 256");
+  XMH3_REQUIRE(D % head_dim == 0, "norm_rope: row width must be a multiple of head_dim");
+  XMH3_REQUIRE(ldx % 8 == 0 && ldo % 8 == 0, "norm_rope: strides must be multiples of 8");
+  XMH3_REQUIRE(dtype == mod_dtype || (scale == nullptr && shift == nullptr),
+               "norm_rope: scale/shift must have the dtype of x");
+  XMH3_REQUIRE(aligned16(x0) && aligned16(o0) && (!x1 || (aligned16(x1) && aligned16(o1))) &&
+                   aligned16(freqs),
+               "norm_rope: pointers must be 16-byte aligned");
+  XMH3_REQUIRE(mod_group >= 1, "norm_rope: modulation group must be >= 1");
+  RowArgs a{};
+  a.x0 = x0; a.o0 = o0; a.x1 = x1; a.o1 = o1; a.ldx = ldx; a.ldo = ldo; a.rows = rows; a.D = D;
+  a.scale = scale; a.shift = shift; a.mod_ld = mod_ld; a.row_map = nullptr; a.mod_group = mod_group;
+  a.freqs = freqs; a.freqs_row_stride = freqs_row_stride; a.head_dim = head_dim; a.eps = eps;
+  const bool adaln = scale != nullptr;
+  XMH3_REQUIRE(adaln == (shift != nullptr), "norm_rope: scale and shift go together");
+#define XMH3_NR(TX, TF)                                                                          \
+  {                                                                                              \
+    if (adaln) {                                                                                 \
+      if (head_dim == 128) return launch_row<TX, TX, TF, true, true, false, 8>(a, st);           \
+      if (head_dim == 64) return launch_row<TX, TX, TF, true, true, false, 4>(a, st);            \
+      return launch_row<TX, TX, TF, true, true, false, 16>(a, st);                               \
+    }                                                                                            \
+    if (head_dim == 128) return launch_row<TX, TX, TF, true, false, false, 8>(a, st);            \
+    if (head_dim == 64) return launch_row<TX, TX, TF, true, false, false, 4>(a, st);             \
+    return launch_row<TX, TX, TF, true, false, false, 16>(a, st);                                \
+  }
+  if (dtype == DT_BF16 && freqs_dtype == DT_F32) XMH3_NR(BF16T, F32T)
+  if (dtype == DT_BF16 && freqs_dtype == DT_BF16) XMH3_NR(BF16T, BF16T)
+  if (dtype == DT_F16 && freqs_dtype == DT_F32) XMH3_NR(F16T, F32T)
+  if (dtype == DT_F16 && freqs_dtype == DT_F16) XMH3_NR(F16T, F16T)
+#undef XMH3_NR
+  return fail(XMH3_EUNSUPPORTED, "norm_rope: dtype combination not supported (x bf16/fp16; table fp32 or x's dtype)");
+}
+
+int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D, int64_t ldx,
+                   int64_t ldo, const void* weight, const void* scale, const void* shift,
+                   int mod_dtype, int64_t mod_ld, const int32_t* row_map, int64_t mod_group,
+                   float eps, hipStream_t st) {
+  XMH3_REQUIRE(rows >= 0 && D > 0, "rms_adaln: bad sizes");
+  if (rows == 0) return XMH3_OK;
+  XMH3_REQUIRE(x && out && scale && shift, "rms_adaln: null pointer");
+  XMH3_REQUIRE(D % 8 == 0 && ldx % 8 == 0 && ldo % 8 == 0 && mod_ld % 8 == 0,
+               "rms_adaln: width and strides must be multiples of 8");
+  XMH3_REQUIRE(aligned16(x) && aligned16(out) && aligned16(scale) && aligned16(shift) &&
+                   (!weight || aligned16(weight)),
+               "rms_adaln: pointers must be 16-byte aligned");
+  XMH3_REQUIRE(row_map || mod_group >= 1, "rms_adaln: modulation group must be >= 1");
+  RowArgs a{};
+  a.x0 = x; a.o0 = out; a.ldx = ldx; a.ldo = ldo; a.rows = rows; a.D = D; a.weight = weight;
+  a.scale = scale; a.shift = shift; a.mod_ld = mod_ld; a.row_map = row_map; a.mod_group = mod_group;
+  a.eps = eps;
+#define XMH3_RA(TX, TM)                                                          \
+  {                                                                              \
+    if (weight) return launch_row<TX, TM, F32T, false, true, true, 1>(a, st);    \
+    return launch_row<TX, TM, F32T, false, true, false, 1>(a, st);               \
+  }
+  if (dtype == DT_BF16 && mod_dtype == DT_BF16) XMH3_RA(BF16T, BF16T)
+  if (dtype == DT_BF16 && mod_dtype == DT_F32) XMH3_RA(BF16T, F32T)
+  if (dtype == DT_F16 && mod_dtype == DT_F16) XMH3_RA(F16T, F16T)
+  if (dtype == DT_F16 && mod_dtype == DT_F32) XMH3_RA(F16T, F32T)
+  if (dtype == DT_F32 && mod_dtype == DT_F32) XMH3_RA(F32T, F32T)
+#undef XMH3_RA
+  return fail(XMH3_EUNSUPPORTED, "rms_adaln: dtype combination not supported");
+}
+
+template <typename TX, typename TW, typename TF, bool NORM>
+static int launch_head(HeadArgs& a, int lph, hipStream_t st) {
+  const int64_t nheads = a.B * a.S * a.H;
+#define XMH3_H(L)                                                                               \
+  if (lph == L) {                                                                               \
+    dim3 grid((unsigned)((nheads + (256 / L) - 1) / (256 / L)));                                \
+    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L>), grid, dim3(256), 0, st, a);      \
+    return check_launch("headspan_kernel");                                                     \
+  }
+  XMH3_H(1) XMH3_H(2) XMH3_H(4) XMH3_H(8) XMH3_H(16) XMH3_H(32) XMH3_H(64)
+#undef XMH3_H
+  return fail(XMH3_EUNSUPPORTED, "head-span kernel: head too wide");
+}
+
+int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+               const int64_t* xstrides, const int64_t* ostrides, const void* weight,
+               int weight_dtype, const void* freqs, int freqs_dtype, const int64_t* fstrides,
+               int rot_dim, float eps, int norm, hipStream_t st) {
+  XMH3_REQUIRE(B >= 0 && S >= 0 && H >= 0 && D > 0, "rope: bad sizes");
+  if (B * S * H == 0) return XMH3_OK;
+  const int rot = rot_dim ? rot_dim : (int)D;
+  XMH3_REQUIRE(rot > 0 && rot <= D && rot % 16 == 0 && (D - rot) % 8 == 0,
+               "rope: rot_dim must be a multiple of 16 and (head_dim - rot_dim) a multiple of 8");
+  XMH3_REQUIRE(x && out && freqs && (!norm || weight), "rope: null pointer");
+  for (int i = 0; i < 3; ++i)
+    XMH3_REQUIRE(xstrides[i] % 8 == 0 && ostrides[i] % 8 == 0 && fstrides[i] % 8 == 0,
+                 "rope: strides must be multiples of 8 elements");
+  XMH3_REQUIRE(aligned16(x) && aligned16(out) && aligned16(freqs) && (!weight || aligned16(weight)),
+               "rope: pointers must be 16-byte aligned");
+  const int items = rot / 16 + (int)(D - rot) / 8;
+  int lph = 1;
+  while (lph < items) lph <<= 1;
+  XMH3_REQUIRE(lph <= 64, "rope: head_dim too large");
+  HeadArgs a{};
+  a.x = x; a.out = out; a.B = B; a.S = S; a.H = H; a.D = D;
+  a.sb = xstrides[0]; a.ss = xstrides[1]; a.sh = xstrides[2];
+  a.ob = ostrides[0]; a.os = ostrides[1]; a.oh = ostrides[2];
+  a.weight = weight; a.freqs = freqs; a.fb = fstrides[0]; a.fs = fstrides[1]; a.fh = fstrides[2];
+  a.rot = rot; a.eps = eps;
+  XMH3_REQUIRE(!norm || weight_dtype == dtype || weight_dtype == DT_F32,
+               "rope: norm weight must have x's dtype or fp32");
+#define XMH3_HD(TX, TF)                                                                   \
+  {                                                                                       \
+    if (!norm) return launch_head<TX, TX, TF, false>(a, lph, st);                         \
+    if (weight_dtype == DT_F32) return launch_head<TX, F32T, TF, true>(a, lph, st);        \
+    return launch_head<TX, TX, TF, true>(a, lph, st);                                     \
+  }
+  if (dtype == DT_BF16 && freqs_dtype == DT_F32) XMH3_HD(BF16T, F32T)
+  if (dtype == DT_BF16 && freqs_dtype == DT_BF16) XMH3_HD(BF16T, BF16T)
+  if (dtype == DT_F16 && freqs_dtype == DT_F32) XMH3_HD(F16T, F32T)
+  if (dtype == DT_F16 && freqs_dtype == DT_F16) XMH3_HD(F16T, F16T)
+  if (dtype == DT_F32 && freqs_dtype == DT_F32) XMH3_HD(F32T, F32T)
+#undef XMH3_HD
+  return fail(XMH3_EUNSUPPORTED, "rope: dtype combination not supported");
+}
+
+}  // namespace xmh3
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" int xmh3_norm_rope(const void* q_in, void* q_out, const void* k_in, void* k_out, int dtype,
+                              int64_t tokens, int64_t width, int64_t ld_in, int64_t ld_out,
+                              const void* scale, const void* shift, int mod_dtype, int64_t mod_ld,
+                              int64_t mod_group, const void* freqs, int freqs_dtype,
+                              int64_t freqs_token_stride, int head_dim, float eps,
+                              hipStream_t stream) {
+  return xmh3::norm_rope_rows(q_in, q_out, k_in, k_out, dtype, tokens, width, ld_in, ld_out, scale,
+                              shift, mod_dtype, mod_ld, mod_group, freqs, freqs_dtype,
+                              freqs_token_stride, head_dim, eps, stream);
+}
+
+extern "C" int xmh3_rms_adaln(const void* x, void* out, int dtype, int64_t rows, int64_t width,
+                              int64_t ld_in, int64_t ld_out, const void* norm_weight,
+                              const void* scale, const void* shift, int mod_dtype, int64_t mod_ld,
+                              const int32_t* row_map, int64_t mod_group, float eps,
+                              hipStream_t stream) {
+  return xmh3::rms_adaln_rows(x, out, dtype, rows, width, ld_in, ld_out, norm_weight, scale, shift,
+                              mod_dtype, mod_ld, row_map, mod_group, eps, stream);
+}
+
+extern "C" int xmh3_rope_split_half(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H,
+                                    int64_t head_dim, const int64_t* x_strides,
+                                    const int64_t* out_strides, const void* norm_weight,
+                                    int weight_dtype, const void* freqs, int freqs_dtype,
+                                    const int64_t* freqs_strides, int rot_dim, float eps, int norm,
+                                    hipStream_t stream) {
+  return xmh3::rope_heads(x, out, dtype, B, S, H, head_dim, x_strides, out_strides, norm_weight,
+                          weight_dtype, freqs, freqs_dtype, freqs_strides, rot_dim, eps, norm,
+                          stream);
+}

@@ -1,0 +1,284 @@
+// Per-token dynamic int8 quantisation for gfx950.
+//
+// Semantics (bit exact) follow the reference's eager quantizer,
+// CK/backends/eager/quantization.py:815-826,857-875
+// (CK = backends/turbo/vendor/comfy_kitchen):
+//   amax  = max |x| over the row (in x's dtype, exact)
+//   scale = max(amax / 127, 1e-30)          fp32, true division
+//   s_T   = T(scale) (0 -> smallest normal of T)
+//   v     = T(float(x) / float(s_T))        correctly rounded fp32 divide
+//   q     = clamp(rint(v), -128, 127)       ties to even
+// and returns the unrounded fp32 scale. An optional input activation
+// (GELU-tanh, CK/backends/_activations.py:40-53) is applied first and
+// rounded to T, as the reference materialises it.
+//
+// Layout: one wave64 per row, the whole row held in VGPRs (16-byte loads,
+// 8 elements per lane per step), so the row is read from HBM exactly once.
+// A block-per-row two-pass kernel covers rows wider than the register path.
+#include "common.hpp"
+
+namespace xmh3 {
+
+// 8 elements of T as raw storage
+template <typename T> struct Pack8;
+template <> struct Pack8<BF16T> { uint4 v; };
+template <> struct Pack8<F16T> { uint4 v; };
+template <> struct Pack8<F32T> { uint4 v[2]; };
+
+template <typename T>
+__device__ __forceinline__ void load8(const typename T::storage* p, Pack8<T>& d) {
+  if constexpr (sizeof(typename T::storage) == 2) {
+    d.v = *reinterpret_cast<const uint4*>(p);
+  } else {
+    d.v[0] = *reinterpret_cast<const uint4*>(p);
+    d.v[1] = *reinterpret_cast<const uint4*>(p + 4);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float get8(const Pack8<T>& d, int j) {
+  if constexpr (sizeof(typename T::storage) == 2) {
+    uint32_t w = (&d.v.x)[j >> 1];
+    return T::load((j & 1) ? (w >> 16) : (w & 0xffffu));
+  } else {
+    return __uint_as_float((&d.v[j >> 2].x)[j & 3]);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void set8(Pack8<T>& d, int j, float f) {
+  if constexpr (sizeof(typename T::storage) == 2) {
+    uint32_t& w = (&d.v.x)[j >> 1];
+    uint32_t b = T::store(f);
+    w = (j & 1) ? ((w & 0xffffu) | (b << 16)) : ((w & 0xffff0000u) | b);
+  } else {
+    (&d.v[j >> 2].x)[j & 3] = __float_as_uint(f);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ int quant_code_T(float x, float sT) {
+  float v = T::round(x / sT);
+  float r = rintf(v);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return (int)r;
+}
+
+template <typename T>
+__device__ __forceinline__ float scale_for_math(float scale) {
+  float sT = T::round(scale);
+  return sT == 0.0f ? T::tiny() : sT;
+}
+
+__device__ __forceinline__ float row_scale(float amax) {
+  float s = amax / 127.0f;
+  return s < 1e-30f ? 1e-30f : s;
+}
+
+// ---------------------------------------------------------------------------
+// register-resident path: NL steps of 512 elements per row
+// ---------------------------------------------------------------------------
+template <typename T, int ACT, int NL>
+__global__ __launch_bounds__(256) void quant_rows_reg_kernel(
+    const typename T::storage* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    uint32_t* __restrict__ zero_rows) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const typename T::storage* xr = x + row * ldx;
+  Pack8<T> buf[NL];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int64_t col = ((int64_t)i * 64 + lane) * 8;
+    if (col < K) {
+      load8<T>(xr + col, buf[i]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float f = get8<T>(buf[i], j);
+        if constexpr (ACT == ACT_GELU_TANH) {
+          f = T::round(gelu_tanh_f32(f));
+          set8<T>(buf[i], j, f);
+        }
+        amax = fmaxf(amax, fabsf(f));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  const float s = row_scale(amax);
+  const float sT = scale_for_math<T>(s);
+  int8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int64_t col = ((int64_t)i * 64 + lane) * 8;
+    if (col < K) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_T<T>(get8<T>(buf[i], j), sT) & 0xff) << (8 * j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) hi |= (uint32_t)(quant_code_T<T>(get8<T>(buf[i], j + 4), sT) & 0xff) << (8 * j);
+      *reinterpret_cast<uint2*>(qr + col) = make_uint2(lo, hi);
+    }
+  }
+  if (lane == 0) {
+    scale[row] = s;
+    if (zero_rows) zero_rows[row] = 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// generic path: one 256-thread block per row, two passes over the row
+// (any K; the second pass re-reads the row, mostly from L2)
+// ---------------------------------------------------------------------------
+template <typename T, int ACT>
+__global__ __launch_bounds__(256) void quant_rows_generic_kernel(
+    const typename T::storage* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    uint32_t* __restrict__ zero_rows) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const typename T::storage* xr = x + row * ldx;
+  float amax = 0.0f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) {
+    float f = T::load(xr[k]);
+    if constexpr (ACT == ACT_GELU_TANH) f = T::round(gelu_tanh_f32(f));
+    amax = fmaxf(amax, fabsf(f));
+  }
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = row_scale(amax);
+  const float sT = scale_for_math<T>(s);
+  int8_t* qr = q + row * ldq;
+  for (int64_t k = threadIdx.x; k < K; k += 256) {
+    float f = T::load(xr[k]);
+    if constexpr (ACT == ACT_GELU_TANH) f = T::round(gelu_tanh_f32(f));
+    qr[k] = (int8_t)quant_code_T<T>(f, sT);
+  }
+  if (threadIdx.x == 0) {
+    scale[row] = s;
+    if (zero_rows) zero_rows[row] = 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// requant with a precomputed row amax (bit pattern of the bf16 |g| maximum,
+// produced by the fused fc1 epilogue): a pure streaming pass, 8 elements per
+// thread, 16-byte loads and 8-byte stores.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void requant_rows_kernel(
+    const typename T::storage* __restrict__ g, int64_t ldg, int64_t M, int64_t K,
+    const uint32_t* __restrict__ row_amax, int8_t* __restrict__ q, int64_t ldq,
+    float* __restrict__ scale) {
+  const int64_t per_row = K >> 3;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * per_row) return;
+  const int64_t row = idx / per_row;
+  const int64_t col = (idx - row * per_row) << 3;
+  const float s = row_scale(__uint_as_float(row_amax[row]));
+  const float sT = scale_for_math<T>(s);
+  Pack8<T> b;
+  load8<T>(g + row * ldg + col, b);
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_T<T>(get8<T>(b, j), sT) & 0xff) << (8 * j);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) hi |= (uint32_t)(quant_code_T<T>(get8<T>(b, j + 4), sT) & 0xff) << (8 * j);
+  *reinterpret_cast<uint2*>(q + row * ldq + col) = make_uint2(lo, hi);
+  if (col == 0) scale[row] = s;
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+template <typename T, int ACT>
+static int launch_quant_T(const void* x, int64_t ldx, int64_t M, int64_t K, int8_t* q,
+                          int64_t ldq, float* scale, uint32_t* zero_rows, hipStream_t st) {
+  using S = typename T::storage;
+  const S* xs = static_cast<const S*>(x);
+  const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) &&
+                      ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
+  const int64_t steps = (K + 511) / 512;
+  if (vec_ok && steps <= 32) {
+    dim3 grid((unsigned)((M + 3) / 4));
+#define XMH3_Q(NLV)                                                                                \
+  if (steps <= NLV) {                                                                              \
+    hipLaunchKernelGGL((quant_rows_reg_kernel<T, ACT, NLV>), grid, dim3(256), 0, st, xs, ldx, M, K, \
+                       q, ldq, scale, zero_rows);                                                  \
+    return check_launch("quant_rows_reg_kernel");                                                  \
+  }
+    XMH3_Q(1) XMH3_Q(2) XMH3_Q(3) XMH3_Q(4) XMH3_Q(6) XMH3_Q(8) XMH3_Q(10) XMH3_Q(12) XMH3_Q(16)
+    XMH3_Q(20) XMH3_Q(24) XMH3_Q(28) XMH3_Q(32)
+#undef XMH3_Q
+  }
+  hipLaunchKernelGGL((quant_rows_generic_kernel<T, ACT>), dim3((unsigned)M), dim3(256), 0, st, xs,
+                     ldx, M, K, q, ldq, scale, zero_rows);
+  return check_launch("quant_rows_generic_kernel");
+}
+
+int quantize_rows(const void* x, int x_dtype, int input_act, int64_t M, int64_t K, int64_t ldx,
+                  int8_t* q, int64_t ldq, float* scale, uint32_t* zero_rows, hipStream_t st) {
+  XMH3_REQUIRE(M >= 0 && K >= 0, "quantize_int8_rowwise: negative size");
+  XMH3_REQUIRE(input_act == ACT_NONE || input_act == ACT_GELU_TANH,
+               "quantize_int8_rowwise: input_act must be none or gelu_tanh");
+  XMH3_REQUIRE(M <= 0x7fffffffLL * 4, "quantize_int8_rowwise: too many rows");
+  if (M == 0) return XMH3_OK;
+  XMH3_REQUIRE(x && q && scale, "quantize_int8_rowwise: null pointer");
+  XMH3_REQUIRE(ldx >= K && ldq >= K, "quantize_int8_rowwise: leading dimension < K");
+  switch (x_dtype) {
+    case DT_BF16:
+      return input_act ? launch_quant_T<BF16T, ACT_GELU_TANH>(x, ldx, M, K, q, ldq, scale, zero_rows, st)
+                       : launch_quant_T<BF16T, ACT_NONE>(x, ldx, M, K, q, ldq, scale, zero_rows, st);
+    case DT_F16:
+      return input_act ? launch_quant_T<F16T, ACT_GELU_TANH>(x, ldx, M, K, q, ldq, scale, zero_rows, st)
+                       : launch_quant_T<F16T, ACT_NONE>(x, ldx, M, K, q, ldq, scale, zero_rows, st);
+    case DT_F32:
+      return input_act ? launch_quant_T<F32T, ACT_GELU_TANH>(x, ldx, M, K, q, ldq, scale, zero_rows, st)
+                       : launch_quant_T<F32T, ACT_NONE>(x, ldx, M, K, q, ldq, scale, zero_rows, st);
+    default:
+      return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise: dtype must be fp32, fp16 or bf16");
+  }
+}
+
+int requant_rows(const void* g, int g_dtype, int64_t M, int64_t K, int64_t ldg,
+                 const uint32_t* row_amax, int8_t* q, int64_t ldq, float* scale, hipStream_t st) {
+  XMH3_REQUIRE(M >= 0 && K >= 0, "requant: negative size");
+  if (M == 0 || K == 0) return XMH3_OK;
+  XMH3_REQUIRE(K % 8 == 0 && ldg % 8 == 0 && ldq % 8 == 0, "requant: K and strides must be multiples of 8");
+  XMH3_REQUIRE(g_dtype == DT_BF16 || g_dtype == DT_F16, "requant: dtype must be bf16 or fp16");
+  const int64_t threads = M * (K / 8);
+  dim3 grid((unsigned)((threads + 255) / 256));
+  if (g_dtype == DT_BF16)
+    hipLaunchKernelGGL(requant_rows_kernel<BF16T>, grid, dim3(256), 0, st,
+                       static_cast<const uint16_t*>(g), ldg, M, K, row_amax, q, ldq, scale);
+  else
+    hipLaunchKernelGGL(requant_rows_kernel<F16T>, grid, dim3(256), 0, st,
+                       static_cast<const uint16_t*>(g), ldg, M, K, row_amax, q, ldq, scale);
+  return check_launch("requant_rows_kernel");
+}
+
+}  // namespace xmh3
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" int xmh3_quantize_int8_rowwise(const void* x, int x_dtype, int input_act, int64_t M,
+                                          int64_t K, int64_t ldx, int8_t* q, float* scale,
+                                          hipStream_t stream) {
+  return xmh3::quantize_rows(x, x_dtype, input_act, M, K, ldx, q, K, scale, nullptr, stream);
+}
+
+extern "C" int xmh3_quantize_int8_rowwise_ex(const void* x, int x_dtype, int input_act, int64_t M,
+                                             int64_t K, int64_t ldx, int8_t* q, float* scale,
+                                             uint32_t* clear_rows, hipStream_t stream) {
+  return xmh3::quantize_rows(x, x_dtype, input_act, M, K, ldx, q, K, scale, clear_rows, stream);
+}
+
+extern "C" int xmh3_requant_int8_rows(const void* g, int g_dtype, int64_t M, int64_t K, int64_t ldg,
+                                      const uint32_t* row_absmax_bits, int8_t* q, float* scale,
+                                      hipStream_t stream) {
+  return xmh3::requant_rows(g, g_dtype, M, K, ldg, row_absmax_bits, q, K, scale, stream);
+}

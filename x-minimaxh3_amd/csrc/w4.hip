@@ -1,0 +1,122 @@
+// Grouped int4 weights -> the int8 grid consumed by the int8 GEMM (gfx950).
+//
+// Rule (CK/backends/eager/w4a8_int8.py:344-363, CK = backends/turbo/vendor/
+// comfy_kitchen): byte b holds code[2j] = b & 0xF and code[2j+1] = b >> 4;
+// level = code - 8 (or codebook[code]); w8 = clamp(rint(level * s_rel[n, k/G]),
+// -127, 127) with s_rel read as fp32 (bf16 s_rel widened exactly).
+//
+// Each thread turns 8 packed bytes into 16 int8 through a 16-entry level table
+// built once per (row, group) in registers: every code of a group maps through
+// the same s_rel, so the per-element multiply + rint becomes a lookup.
+#include "common.hpp"
+
+namespace xmh3 {
+
+__device__ __forceinline__ int w4_level_code(float level, float srel) {
+  float r = rintf(level * srel);
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int)r;
+}
+
+template <bool BF16_SREL>
+__device__ __forceinline__ float load_srel(const void* p, int64_t i) {
+  if constexpr (BF16_SREL) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return static_cast<const float*>(p)[i];
+}
+
+// G % 16 == 0: the 16 outputs of a thread share one group
+template <bool BF16_SREL>
+__global__ __launch_bounds__(256) void w4_decode_kernel(const uint8_t* __restrict__ packed,
+                                                        const void* __restrict__ s_rel,
+                                                        const float* __restrict__ codebook,
+                                                        int64_t N, int64_t K, int64_t G,
+                                                        int8_t* __restrict__ out) {
+  const int64_t per_row = K / 16;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= N * per_row) return;
+  const int64_t n = idx / per_row;
+  const int64_t k0 = (idx - n * per_row) * 16;
+  const float s = load_srel<BF16_SREL>(s_rel, n * (K / G) + k0 / G);
+  // 16-entry table: byte c of lut[c/4] is the int8 for code c
+  uint32_t lut[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int c = w * 4 + b;
+      const float level = codebook ? codebook[c] : (float)(c - 8);
+      word |= (uint32_t)(w4_level_code(level, s) & 0xff) << (8 * b);
+    }
+    lut[w] = word;
+  }
+  const uint2 p = *reinterpret_cast<const uint2*>(packed + n * (K / 2) + k0 / 2);
+  uint32_t o[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t src = (w < 2) ? p.x : p.y;
+    const uint32_t two = (src >> (16 * (w & 1))) & 0xffffu;  // 2 bytes -> 4 codes
+    uint32_t word = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (two >> (8 * (b >> 1))) & 0xffu;
+      const uint32_t code = (b & 1) ? (byte >> 4) : (byte & 0xf);
+      const uint32_t val = (lut[code >> 2] >> (8 * (code & 3))) & 0xffu;
+      word |= val << (8 * b);
+    }
+    o[w] = word;
+  }
+  *reinterpret_cast<uint4*>(out + n * K + k0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// any G (>= 2, dividing K): one byte (two outputs) per thread
+template <bool BF16_SREL>
+__global__ __launch_bounds__(256) void w4_decode_generic_kernel(const uint8_t* __restrict__ packed,
+                                                                const void* __restrict__ s_rel,
+                                                                const float* __restrict__ codebook,
+                                                                int64_t N, int64_t K, int64_t G,
+                                                                int8_t* __restrict__ out) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= N * (K / 2)) return;
+  const int64_t n = idx / (K / 2);
+  const int64_t k = (idx - n * (K / 2)) * 2;
+  const uint32_t byte = packed[idx];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = h ? (int)(byte >> 4) : (int)(byte & 0xf);
+    const float s = load_srel<BF16_SREL>(s_rel, n * (K / G) + (k + h) / G);
+    const float level = codebook ? codebook[c] : (float)(c - 8);
+    out[n * K + k + h] = (int8_t)w4_level_code(level, s);
+  }
+}
+
+int w4_decode(const uint8_t* packed, const void* s_rel, int s_rel_dtype, const float* codebook,
+              int64_t N, int64_t K, int64_t G, int8_t* out, hipStream_t st) {
+  XMH3_REQUIRE(N >= 0 && K >= 0 && G > 0, "w4_decode: bad sizes");
+  if (N == 0 || K == 0) return XMH3_OK;
+  XMH3_REQUIRE(K % 2 == 0 && K % G == 0, "w4_decode: K must be even and a multiple of group_size");
+  XMH3_REQUIRE(packed && s_rel && out, "w4_decode: null pointer");
+  XMH3_REQUIRE(s_rel_dtype == DT_F32 || s_rel_dtype == DT_BF16, "w4_decode: s_rel must be fp32 or bf16");
+  const bool bf = s_rel_dtype == DT_BF16;
+  const bool fast = (G % 16 == 0) && ((uintptr_t)packed % 8 == 0) && ((uintptr_t)out % 16 == 0);
+  if (fast) {
+    const int64_t threads = N * (K / 16);
+    dim3 grid((unsigned)((threads + 255) / 256));
+    if (bf) hipLaunchKernelGGL(w4_decode_kernel<true>, grid, dim3(256), 0, st, packed, s_rel, codebook, N, K, G, out);
+    else hipLaunchKernelGGL(w4_decode_kernel<false>, grid, dim3(256), 0, st, packed, s_rel, codebook, N, K, G, out);
+    return check_launch("w4_decode_kernel");
+  }
+  const int64_t threads = N * (K / 2);
+  dim3 grid((unsigned)((threads + 255) / 256));
+  if (bf) hipLaunchKernelGGL(w4_decode_generic_kernel<true>, grid, dim3(256), 0, st, packed, s_rel, codebook, N, K, G, out);
+  else hipLaunchKernelGGL(w4_decode_generic_kernel<false>, grid, dim3(256), 0, st, packed, s_rel, codebook, N, K, G, out);
+  return check_launch("w4_decode_generic_kernel");
+}
+
+}  // namespace xmh3
+
+extern "C" int xmh3_w4_decode_int8(const uint8_t* packed, const void* s_rel, int s_rel_dtype,
+                                   const float* codebook, int64_t N, int64_t K, int64_t group_size,
+                                   int8_t* out, hipStream_t stream) {
+  return xmh3::w4_decode(packed, s_rel, s_rel_dtype, codebook, N, K, group_size, out, stream);
+}

@@ -1,0 +1,90 @@
+"""Drop-in adapters for the H3 engine's call sites of the hot path.
+
+* ``mi355x_int8_kernel`` / ``mi355x_w4a8_kernel`` have the ``Int8Kernel`` and
+  ``W4A8Kernel`` callable signatures the engine injects into every quantized
+  linear (h3serve/native_engine/model/quantization.py:19-37, injected via
+  assembly.py:166-228).
+* ``rms_adaln(value, norm, shift, scale, segments)`` is the segmented
+  RMSNorm + AdaLN of h3serve/native_engine/model/kernels.py:7586-7634 in one
+  launch (row map per token instead of one launch per segment).
+* ``apply_qknorm_rope(query, key, *, q_weight, k_weight, frequencies, eps)``
+  is the table form of h3serve/native_engine/model/layers.py:72-100.
+* ``segment_row_map`` follows h3serve/native_engine/model/fused_mlp.py:34-55.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import backend, ops
+
+_ROW_MAPS: dict[tuple, torch.Tensor] = {}
+
+
+def segment_row_map(length: int, segments, device) -> torch.Tensor:
+    """int32 [length]: the modulation row of each token; segments must be an
+    ordered partition ``(start, stop, row)`` of [0, length)."""
+    norm = tuple((int(a), int(b), int(r)) for a, b, r in segments)
+    dev = torch.device(device)
+    key = (dev.type, dev.index, int(length), norm)
+    hit = _ROW_MAPS.get(key)
+    if hit is not None:
+        return hit
+    host = torch.empty(length, dtype=torch.int32)
+    prev = 0
+    for a, b, r in norm:
+        if a != prev or b <= a:
+            raise ValueError("modulation segments must be an ordered partition")
+        host[a:b] = r
+        prev = b
+    if prev != length:
+        raise ValueError("modulation segments do not cover the packed sequence")
+    out = host.to(dev)
+    _ROW_MAPS[key] = out
+    return out
+
+
+def rms_adaln(value: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tensor, segments,
+              *, eps: float | None = None) -> torch.Tensor:
+    """RMSNorm(value) then per-segment ``* (1 + scale[row]) + shift[row]``.
+    ``norm`` is an RMSNorm module (``.weight``, ``.eps``) or a weight tensor
+    (then ``eps`` is required)."""
+    weight = getattr(norm, "weight", norm)
+    if eps is None:
+        eps = getattr(norm, "eps", None)
+        if eps is None:
+            raise ValueError("eps is required when norm is a tensor")
+    if value.ndim != 2:
+        raise ValueError("value must be [tokens, width]")
+    row_map = segment_row_map(value.shape[0], segments, value.device)
+    return backend.rms_adaln_rows(value, weight, scale.to(value.dtype), shift.to(value.dtype), row_map, eps)
+
+
+def apply_qknorm_rope(query: torch.Tensor, key: torch.Tensor, *, q_weight: torch.Tensor, k_weight: torch.Tensor,
+                      frequencies: torch.Tensor, eps: float):
+    """Per-head RMSNorm then split-half partial RoPE, in place, for the packed
+    [1, S, 1, rot/2, 2, 2] table form."""
+    if frequencies.ndim != 6:
+        raise NotImplementedError("the angle-table form of apply_qknorm_rope is not implemented")
+    rot = int(frequencies.shape[-3]) * 2
+    q4, k4 = query.unsqueeze(0), key.unsqueeze(0)
+    ops.rms_rope_split_half_(q4, k4, frequencies, q_weight.to(device=query.device, dtype=query.dtype),
+                             k_weight.to(device=key.device, dtype=key.dtype), epsilon=eps, rot_dim=rot)
+    return q4[0], k4[0]
+
+
+def mi355x_int8_kernel(value: torch.Tensor, qweight: torch.Tensor, scale: torch.Tensor,
+                       bias: torch.Tensor | None, convrot_group_size: int) -> torch.Tensor:
+    """``Int8Kernel``: int8_linear(value, qweight, scale, bias, value.dtype,
+    convrot=bool(convrot_group_size), ...)."""
+    return ops.int8_linear(value, qweight, scale, bias, value.dtype, convrot=bool(convrot_group_size),
+                           convrot_groupsize=convrot_group_size or 256)
+
+
+def mi355x_w4a8_kernel(value, qdata, s_rel, s_channel, codebook, correction, bias, group_size,
+                       convrot_group_size, output_dtype):
+    """``W4A8Kernel``: w4a8_int8_linear with the engine's arguments (a zero
+    convrot group size selects the unrotated form)."""
+    return ops.w4a8_int8_linear(value, qdata, s_rel, s_channel, codebook=codebook, correction=correction,
+                                bias=bias, group_size=group_size, convrot_groupsize=convrot_group_size or 256,
+                                out_dtype=output_dtype, convrot=bool(convrot_group_size))
