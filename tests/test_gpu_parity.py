@@ -25,7 +25,8 @@ def say(msg):
 
 
 def cos_sim(a, b):
-    return F.cosine_similarity(a.float().flatten(), b.float().flatten(), dim=0).item()
+    a, b = a.double().flatten(), b.double().flatten()
+    return (a @ b / (a.norm() * b.norm())).item()
 
 
 def close(got, want, what):
@@ -35,6 +36,18 @@ def close(got, want, what):
     exact = (got == want).float().mean().item() if want.numel() else 1.0
     say(f"  {what}: max|d|={d:.3e} cos={c:.7f} exact={exact:.5f}")
     assert d <= MAX_ABS and c >= MIN_COS, (what, d, c)
+
+
+def same(got, want, what=""):
+    """Bit-exact check that prints a few mismatching elements on failure."""
+    got = got.cpu()
+    eq = torch.equal(got, want)
+    if not eq:
+        idx = (got != want).nonzero()[:6]
+        say(f"  {what} mismatches: {(got != want).sum().item()} of {want.numel()}")
+        for i in idx.tolist():
+            say(f"    at {i}: got {got[tuple(i)].item()!r} want {want[tuple(i)].item()!r}")
+    return eq
 
 
 def outlier_acts(m, k, seed=0, n_out=8, dtype=torch.bfloat16):
@@ -127,7 +140,7 @@ def test_int8_linear_bit_exact(pkg, dev, out_dtype, per_channel, with_bias):
     torch.cuda.synchronize()
     yr = cpu_ref.int8_linear(x, w, sw, bias=bias, out_dtype=out_dtype)
     assert y.dtype == out_dtype
-    assert torch.equal(y.cpu(), yr), (y.cpu() != yr).sum().item()
+    assert same(y, yr, "int8_linear")
 
 
 def test_int8_linear_leading_dims_and_strided_input(pkg, dev):

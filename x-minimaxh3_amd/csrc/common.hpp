@@ -33,13 +33,30 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// fp16 <-> fp32 in integer/fp32 arithmetic only, so subnormal fp16 values are
+// rounded (nearest even) and widened exactly whatever the wave's f16 denormal
+// mode is. Subnormal results come from one fp32 add: |f| + 0.5 places the fp16
+// subnormal ulp (2^-24) at the last fp32 mantissa bit.
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
-  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
-  return (float)v;
+  const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0) {
+    const float v = (float)m * 5.9604644775390625e-08f;  // m * 2^-24, exact
+    return s ? -v : v;
+  }
+  if (e == 31) return __uint_as_float(s | 0x7f800000u | (m << 13));
+  return __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
 }
-__device__ __forceinline__ uint32_t f32_to_f16(float f) {
-  _Float16 v = (_Float16)f;  // v_cvt_f16_f32, round to nearest even
-  return (uint32_t)__builtin_bit_cast(uint16_t, v);
+__device__ __forceinline__ uint32_t f32_to_f16(float ff) {
+  // branch-free: all three cases are computed and selected, so the function
+  // can sit inside fully unrolled epilogue loops
+  uint32_t f = __float_as_uint(ff);
+  const uint32_t sign = f & 0x80000000u;
+  f ^= sign;
+  const uint32_t big = (f > (255u << 23)) ? 0x7e00u : 0x7c00u;                // >= 65536, inf, nan
+  const uint32_t sub = __float_as_uint(__uint_as_float(f) + 0.5f) - 0x3f000000u;  // < 2^-14
+  const uint32_t nrm = (f + 0xc8000fffu + ((f >> 13) & 1u)) >> 13;             // rebias + RNE
+  const uint32_t o = (f >= (143u << 23)) ? big : ((f < (113u << 23)) ? sub : nrm);
+  return o | (sign >> 16);
 }
 
 // Element-type traits: storage type, fp32 view and rounding back to T.

@@ -19,9 +19,23 @@
 // walks a contiguous, GROUP_M-swizzled band of tiles.
 #include "common.hpp"
 
+#include <utility>
+
 namespace xmh3 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Compile-time loop: f(std::integral_constant<int, I>{}) for I in [0, N).
+// Accumulator blocks are addressed only through these constants, so they can
+// never become a dynamically indexed (scratch) array.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 enum Epi : int { EPI_DEQUANT = 0, EPI_GELU = 1, EPI_INT32 = 2 };
 
@@ -83,6 +97,71 @@ __device__ __forceinline__ void store4(uint16_t* p, const float* v, F16T) {
 }
 __device__ __forceinline__ void store4(float* p, const float* v, F32T) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Epilogue shared by both main loops. Lane holds, for block (i, j): row
+// m = m0 + wm*128 + i*16 + lane%16, columns n = n0 + wn*128 + j*16 +
+// 4*(lane/16) + {0..3}. Straight-line code only (compile-time block indices,
+// guards as predicates) so the accumulators stay in registers.
+template <int EPI, typename TO, bool VEC_OUT>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], int m0, int n0, int wm, int wn,
+                                         int lane) {
+  const int em = m0 + wm * 128 + (lane & 15);
+  const int en = n0 + wn * 128 + 4 * (lane >> 4);
+  static_for<8>([&](auto I) {
+    constexpr int i = I;
+    const int m = em + i * 16;
+    const bool mok = m < p.M;
+    float amax = 0.0f;
+    float sxm = 0.0f;
+    if constexpr (EPI != EPI_INT32) sxm = mok ? p.sx[m] : 0.0f;
+    static_for<8>([&](auto J) {
+      constexpr int j = J;
+      const int n = en + j * 16;
+      if constexpr (EPI == EPI_INT32) {
+        int32_t* orow = static_cast<int32_t*>(p.out) + (int64_t)m * p.ldo;
+        if (mok) {
+          if (VEC_OUT && n + 3 < p.N) {
+            *reinterpret_cast<v4i*>(orow + n) = acc[i][j];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n + r < p.N) orow[n + r] = acc[i][j][r];
+          }
+        }
+      } else {
+        typename TO::storage* orow = static_cast<typename TO::storage*>(p.out) + (int64_t)m * p.ldo;
+        const typename TO::storage* brow = static_cast<const typename TO::storage*>(p.bias);
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool nok = n + r < p.N;
+          const float swn = p.sw_per_channel ? (nok ? p.sw[n + r] : 0.0f) : p.sw[0];
+          float y = TO::round((float)acc[i][j][r] * (sxm * swn));
+          if (brow) y = TO::round(y + (nok ? TO::load(brow[n + r]) : 0.0f));
+          if constexpr (EPI == EPI_GELU) {
+            y = TO::round(gelu_tanh_f32(y));
+            amax = fmaxf(amax, nok ? fabsf(y) : 0.0f);
+          }
+          v[r] = y;
+        }
+        if (mok) {
+          if (VEC_OUT && n + 3 < p.N) {
+            store4(orow + n, v, TO{});
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (n + r < p.N) orow[n + r] = (typename TO::storage)TO::store(v[r]);
+          }
+        }
+      }
+    });
+    if constexpr (EPI == EPI_GELU) {
+      amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+      amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+      if (lane < 16 && mok) atomicMax(p.row_amax + m, __float_as_uint(amax));
+    }
+  });
 }
 
 template <int BK, int EPI, typename TO, bool VEC_OUT>
@@ -168,91 +247,138 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_kernel(GemmArgs p) {
         const int r = wn * 128 + j * 16 + frow;
         bf[j] = *reinterpret_cast<const v4i*>(&lds[cur][1][r * BK + swz<BK>(r, kk * 4 + fchunk) * 16]);
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+      static_for<8>([&](auto I) {
+        static_for<8>([&](auto J) {
+          acc[I][J] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[J], af[I], acc[I][J], 0, 0, 0);
+        });
+      });
     }
     if (kt + 1 < ksteps) sstore(cur ^ 1);
     __syncthreads();
   }
 
-  // ---------------------------------------------------------------- epilogue
-  // lane holds, for block (i, j): row m = base_m + i*16 + lane%16,
-  // columns n = base_n + j*16 + 4*(lane/16) + {0..3}.
-  const int em = m0 + wm * 128 + (lane & 15);
-  const int en = n0 + wn * 128 + 4 * (lane >> 4);
-  float amax_row[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) amax_row[i] = 0.0f;
+  epilogue<EPI, TO, VEC_OUT>(p, acc, m0, n0, wm, wn, lane);
+}
 
-  float swv[8][4];
-  if constexpr (EPI != EPI_INT32) {
+// ---------------------------------------------------------------------------
+// main loop v2 (K % 64 == 0): global -> LDS by DMA (global_load_lds_dwordx4),
+// 4 LDS stages of BK = 64, loads issued up to 4 K-steps ahead, no VGPR staging.
+//
+// Stage s holds the A tile [256 rows][64 B] at offset 0 and the B tile at
+// 16 KiB, each row's four 16-byte chunks XOR-swizzled (chunk ^ ((row>>1)&3)).
+// A DMA instruction writes 1 KiB contiguous (lane l -> byte 16*l), i.e. 16
+// rows; the swizzle is applied on the global side by choosing which chunk
+// each lane fetches. Rows past M or N are clamped to the last valid row (their
+// products only reach outputs that are never stored).
+//
+// Synchronisation per K-step t: each wave waits (s_waitcnt) until its own
+// fragment reads of stage t are in registers and its DMA for stage t+1 has
+// landed, then s_barrier (no fence, so the loads of later stages stay in
+// flight); after the barrier no wave reads stage t's buffer any more, so it
+// takes stage t+4.
+// ---------------------------------------------------------------------------
+constexpr int DMA_BK = 64, DMA_STAGES = 4, DMA_STAGE_BYTES = 2 * BM * DMA_BK;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ void wait_vm(int outstanding_stages) {
+  // vmcnt = 8 * stages still allowed in flight (8 DMA instructions per thread
+  // per stage); the expcnt and lgkmcnt fields are left at their maximum
+  if (outstanding_stages >= 3) __builtin_amdgcn_s_waitcnt(0x4f78);       // vmcnt(24)
+  else if (outstanding_stages == 2) __builtin_amdgcn_s_waitcnt(0x4f70);  // vmcnt(16)
+  else if (outstanding_stages == 1) __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
+  else __builtin_amdgcn_s_waitcnt(0x0f70);                               // vmcnt(0)
+}
+
+template <int EPI, typename TO, bool VEC_OUT>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[DMA_STAGES][DMA_STAGE_BYTES];
+
+  int tm, tn;
+  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // DMA sources: wave w fills 16-row blocks b = 4w + i (i < 4) of A and B
+  const int8_t* a_src[4];
+  const int8_t* b_src[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = en + j * 16 + r;
-        swv[j][r] = p.sw_per_channel ? (n < p.N ? p.sw[n] : 0.0f) : p.sw[0];
-      }
+  for (int i = 0; i < 4; ++i) {
+    const int r = (wave * 4 + i) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ ((r >> 1) & 3);
+    const int ar = min(m0 + r, p.M - 1), br = min(n0 + r, p.N - 1);
+    a_src[i] = p.A + (int64_t)ar * p.lda + c * 16;
+    b_src[i] = p.B + (int64_t)br * p.ldb + c * 16;
   }
+  auto issue = [&](int t) {
+    int8_t* base = &lds[t & (DMA_STAGES - 1)][0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(a_src[i] + (int64_t)t * DMA_BK,
+                                       (lds_void_t*)(base + (wave * 4 + i) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __builtin_amdgcn_global_load_lds(b_src[i] + (int64_t)t * DMA_BK,
+                                       (lds_void_t*)(base + BM * DMA_BK + (wave * 4 + i) * 1024), 16, 0, 0);
+  };
+
+  v4i acc[8][8];
+  static_for<8>([&](auto I) { static_for<8>([&](auto J) { acc[I][J] = v4i{0, 0, 0, 0}; }); });
+
+  // fragment offsets within a stage: row = base + lane%16, logical chunk lane/16
+  const int frow = lane & 15, fchunk = lane >> 4;
+  int a_off[8], b_off[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int m = em + i * 16;
-    if (m >= p.M) continue;
-    if constexpr (EPI == EPI_INT32) {
-      int32_t* orow = static_cast<int32_t*>(p.out) + (int64_t)m * p.ldo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int n = en + j * 16;
-        if (VEC_OUT && n + 3 < p.N) {
-          *reinterpret_cast<v4i*>(orow + n) = acc[i][j];
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < p.N) orow[n + r] = acc[i][j][r];
-        }
-      }
-    } else {
-      const float sxm = p.sx[m];
-      typename TO::storage* orow = static_cast<typename TO::storage*>(p.out) + (int64_t)m * p.ldo;
-      const typename TO::storage* brow = static_cast<const typename TO::storage*>(p.bias);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int n = en + j * 16;
-        float v[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float scl = sxm * swv[j][r];
-          float y = TO::round((float)acc[i][j][r] * scl);
-          if (brow && n + r < p.N) y = TO::round(y + TO::load(brow[n + r]));
-          if constexpr (EPI == EPI_GELU) {
-            y = TO::round(gelu_tanh_f32(y));
-            if (n + r < p.N) amax_row[i] = fmaxf(amax_row[i], fabsf(y));
-          }
-          v[r] = y;
-        }
-        if (VEC_OUT && n + 3 < p.N) {
-          store4(orow + n, v, TO{});
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            if (n + r < p.N) orow[n + r] = (typename TO::storage)TO::store(v[r]);
-        }
-      }
-    }
+    const int ra = wm * 128 + i * 16 + frow, rb = wn * 128 + i * 16 + frow;
+    a_off[i] = ra * DMA_BK + ((fchunk ^ ((ra >> 1) & 3)) * 16);
+    b_off[i] = BM * DMA_BK + rb * DMA_BK + ((fchunk ^ ((rb >> 1) & 3)) * 16);
   }
-  if constexpr (EPI == EPI_GELU) {
+
+  // Fragments are double-buffered in registers: while the MFMAs of step t run
+  // on fa/fb[t&1], the LDS reads of step t+1 fill the other set.
+  auto load_frags = [&](int t, v4i (&af)[8], v4i (&bf)[8]) {
+    const int8_t* st = &lds[t & (DMA_STAGES - 1)][0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float a = amax_row[i];
-      a = fmaxf(a, __shfl_xor(a, 16, 64));
-      a = fmaxf(a, __shfl_xor(a, 32, 64));
-      const int m = em + i * 16;
-      if (lane < 16 && m < p.M) atomicMax(p.row_amax + m, __float_as_uint(a));
-    }
+    for (int j = 0; j < 8; ++j) bf[j] = *reinterpret_cast<const v4i*>(st + b_off[j]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) af[i] = *reinterpret_cast<const v4i*>(st + a_off[i]);
+  };
+  v4i fa0[8], fb0[8], fa1[8], fb1[8];
+
+  const int ksteps = p.K / DMA_BK;
+  // prologue: stages 0..3 in flight, wait for stage 0, read its fragments
+#pragma unroll
+  for (int s = 0; s < DMA_STAGES; ++s)
+    if (s < ksteps) issue(s);
+  wait_vm(min(ksteps - 1, DMA_STAGES - 1));
+  asm volatile("s_barrier" ::: "memory");
+  load_frags(0, fa0, fb0);
+
+  // step t: [this wave's fragment reads of step t done] + [stage t+1 landed]
+  // -> barrier (every wave is past its reads of stage t, so its buffer can
+  // take stage t+4) -> refill -> MFMAs of step t with the reads of step t+1
+  // in flight underneath.
+  auto step = [&](int t, v4i (&af)[8], v4i (&bf)[8], v4i (&an)[8], v4i (&bn)[8]) {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
+    if (t + 1 < ksteps) wait_vm(min(ksteps - 2 - t, DMA_STAGES - 2));
+    asm volatile("s_barrier" ::: "memory");
+    if (t + DMA_STAGES < ksteps) issue(t + DMA_STAGES);
+    if (t + 1 < ksteps) load_frags(t + 1, an, bn);
+    static_for<8>([&](auto I) {
+      static_for<8>([&](auto J) {
+        acc[I][J] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[J], af[I], acc[I][J], 0, 0, 0);
+      });
+    });
+  };
+  int t = 0;
+  for (; t + 1 < ksteps; t += 2) {
+    step(t, fa0, fb0, fa1, fb1);
+    step(t + 1, fa1, fb1, fa0, fb0);
   }
+  if (t < ksteps) step(t, fa0, fb0, fa1, fb1);
+  epilogue<EPI, TO, VEC_OUT>(p, acc, m0, n0, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -261,6 +387,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_kernel(GemmArgs p) {
 template <int BK, int EPI, typename TO>
 static int launch_gemm_T(GemmArgs& a, bool vec, hipStream_t st) {
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  if (a.K % DMA_BK == 0) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
+    else
+      hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI, TO, false>), grid, dim3(NTHREADS), 0, st, a);
+    return check_launch("gemm_i8_dma_kernel");
+  }
   if (vec)
     hipLaunchKernelGGL((gemm_i8_kernel<BK, EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
   else
