@@ -54,9 +54,15 @@ struct GemmArgs {
   int tiles_m, tiles_n;
 };
 
+#ifndef XMH3_GROUP_M
+#define XMH3_GROUP_M 8
+#endif
+#ifndef XMH3_NUM_XCD
+#define XMH3_NUM_XCD 8
+#endif
 constexpr int BM = 256, BN = 256, NTHREADS = 256;
-constexpr int GROUP_M = 8;
-constexpr int NUM_XCD = 8;
+constexpr int GROUP_M = XMH3_GROUP_M;   // M-tiles per swizzle group
+constexpr int NUM_XCD = XMH3_NUM_XCD;   // XCDs workgroups are dealt over
 
 // XOR swizzle of the 16-byte chunk index inside an LDS row of BK bytes.
 template <int BK>
@@ -103,9 +109,36 @@ __device__ __forceinline__ void store4(float* p, const float* v, F32T) {
 // m = m0 + wm*128 + i*16 + lane%16, columns n = n0 + wn*128 + j*16 +
 // 4*(lane/16) + {0..3}. Straight-line code only (compile-time block indices,
 // guards as predicates) so the accumulators stay in registers.
+// Row and column scales of a wave's 128x128 sub-tile, all loaded in one batch
+// when the main loop ends (the fragment registers are free then), so the
+// epilogue pays one memory latency instead of one per output element (with one
+// wave per SIMD nothing else hides it).
+struct EpiScales {
+  float sx[8];      // rows m = em + 16 i
+  float sw[8][4];   // columns n = en + 16 j + r
+};
+
+template <int EPI>
+__device__ __forceinline__ void load_scales(const GemmArgs& p, int m0, int n0, int wm, int wn, int lane,
+                                            EpiScales& sc) {
+  if constexpr (EPI != EPI_INT32) {
+    const int em = m0 + wm * 128 + (lane & 15);
+    const int en = n0 + wn * 128 + 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) sc.sx[i] = (em + i * 16 < p.M) ? p.sx[em + i * 16] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = en + j * 16 + r;
+        sc.sw[j][r] = p.sw_per_channel ? (n < p.N ? p.sw[n] : 0.0f) : p.sw[0];
+      }
+  }
+}
+
 template <int EPI, typename TO, bool VEC_OUT>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], int m0, int n0, int wm, int wn,
-                                         int lane) {
+__device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], const EpiScales& sc, int m0,
+                                         int n0, int wm, int wn, int lane) {
   const int em = m0 + wm * 128 + (lane & 15);
   const int en = n0 + wn * 128 + 4 * (lane >> 4);
   static_for<8>([&](auto I) {
@@ -114,7 +147,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], in
     const bool mok = m < p.M;
     float amax = 0.0f;
     float sxm = 0.0f;
-    if constexpr (EPI != EPI_INT32) sxm = mok ? p.sx[m] : 0.0f;
+    if constexpr (EPI != EPI_INT32) sxm = sc.sx[i];
     static_for<8>([&](auto J) {
       constexpr int j = J;
       const int n = en + j * 16;
@@ -136,8 +169,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], in
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool nok = n + r < p.N;
-          const float swn = p.sw_per_channel ? (nok ? p.sw[n + r] : 0.0f) : p.sw[0];
-          float y = TO::round((float)acc[i][j][r] * (sxm * swn));
+          float y = TO::round((float)acc[i][j][r] * (sxm * sc.sw[j][r]));
           if (brow) y = TO::round(y + (nok ? TO::load(brow[n + r]) : 0.0f));
           if constexpr (EPI == EPI_GELU) {
             y = TO::round(gelu_tanh_f32(y));
@@ -257,11 +289,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_kernel(GemmArgs p) {
     __syncthreads();
   }
 
-  epilogue<EPI, TO, VEC_OUT>(p, acc, m0, n0, wm, wn, lane);
+  EpiScales sc;
+  load_scales<EPI>(p, m0, n0, wm, wn, lane, sc);
+  epilogue<EPI, TO, VEC_OUT>(p, acc, sc, m0, n0, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
-// main loop v2 (K % 64 == 0): global -> LDS by DMA (global_load_lds_dwordx4),
+// main loop v2 (K % 128 == 0): global -> LDS by DMA (global_load_lds_dwordx4),
 // 4 LDS stages of BK = 64, loads issued up to 4 K-steps ahead, no VGPR staging.
 //
 // Stage s holds the A tile [256 rows][64 B] at offset 0 and the B tile at
@@ -277,17 +311,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_kernel(GemmArgs p) {
 // flight); after the barrier no wave reads stage t's buffer any more, so it
 // takes stage t+4.
 // ---------------------------------------------------------------------------
-constexpr int DMA_BK = 64, DMA_STAGES = 4, DMA_STAGE_BYTES = 2 * BM * DMA_BK;
+#ifndef XMH3_DMA_STAGES
+#define XMH3_DMA_STAGES 3
+#endif
+#ifndef XMH3_DMA_SCHED
+#define XMH3_DMA_SCHED 1
+#endif
+constexpr int DMA_BK = 64, DMA_STAGES = XMH3_DMA_STAGES, DMA_STAGE_BYTES = 2 * BM * DMA_BK;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
-__device__ __forceinline__ void wait_vm(int outstanding_stages) {
-  // vmcnt = 8 * stages still allowed in flight (8 DMA instructions per thread
-  // per stage); the expcnt and lgkmcnt fields are left at their maximum
-  if (outstanding_stages >= 3) __builtin_amdgcn_s_waitcnt(0x4f78);       // vmcnt(24)
-  else if (outstanding_stages == 2) __builtin_amdgcn_s_waitcnt(0x4f70);  // vmcnt(16)
-  else if (outstanding_stages == 1) __builtin_amdgcn_s_waitcnt(0x0f78);  // vmcnt(8)
-  else __builtin_amdgcn_s_waitcnt(0x0f70);                               // vmcnt(0)
+// s_waitcnt with vmcnt = 8 * n (8 DMA instructions per thread per stage) and
+// the expcnt / lgkmcnt fields at their maximum (no wait on them)
+template <int N>
+__device__ __forceinline__ void wait_vm_n() {
+  constexpr int v = 8 * N;
+  __builtin_amdgcn_s_waitcnt((v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8));
 }
+__device__ __forceinline__ void wait_vm(int outstanding_stages) {
+  if (outstanding_stages >= 4) wait_vm_n<4>();
+  else if (outstanding_stages == 3) wait_vm_n<3>();
+  else if (outstanding_stages == 2) wait_vm_n<2>();
+  else if (outstanding_stages == 1) wait_vm_n<1>();
+  else wait_vm_n<0>();
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
 template <int EPI, typename TO, bool VEC_OUT>
 __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
@@ -300,27 +347,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
 
-  // DMA sources: wave w fills 16-row blocks b = 4w + i (i < 4) of A and B
-  const int8_t* a_src[4];
-  const int8_t* b_src[4];
+  // DMA sources: wave w fills 16-row blocks b = 4w + i (i < 4) of A and B.
+  // Uniform 64-bit bases + per-lane 32-bit offsets (the host guarantees the
+  // operands span < 2^31 bytes), so each DMA is one saddr+voffset load.
+  const int8_t* a_base = p.A + (int64_t)m0 * p.lda;
+  const int8_t* b_base = p.B + (int64_t)n0 * p.ldb;
+  uint32_t a_off_g[4], b_off_g[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = (wave * 4 + i) * 16 + (lane >> 2);
     const int c = (lane & 3) ^ ((r >> 1) & 3);
-    const int ar = min(m0 + r, p.M - 1), br = min(n0 + r, p.N - 1);
-    a_src[i] = p.A + (int64_t)ar * p.lda + c * 16;
-    b_src[i] = p.B + (int64_t)br * p.ldb + c * 16;
+    a_off_g[i] = (uint32_t)(min(r, p.M - 1 - m0) * (int)p.lda + c * 16);
+    b_off_g[i] = (uint32_t)(min(r, p.N - 1 - n0) * (int)p.ldb + c * 16);
   }
-  auto issue = [&](int t) {
-    int8_t* base = &lds[t & (DMA_STAGES - 1)][0];
+  auto issue = [&](int kslice, int slot) __attribute__((always_inline)) {
+    int8_t* base = &lds[slot % DMA_STAGES][0];
+    const int8_t* ab = a_base + (int64_t)kslice * DMA_BK;
+    const int8_t* bb = b_base + (int64_t)kslice * DMA_BK;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(a_src[i] + (int64_t)t * DMA_BK,
-                                       (lds_void_t*)(base + (wave * 4 + i) * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(ab + a_off_g[i], (lds_void_t*)(base + (wave * 4 + i) * 1024), 16, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      __builtin_amdgcn_global_load_lds(b_src[i] + (int64_t)t * DMA_BK,
-                                       (lds_void_t*)(base + BM * DMA_BK + (wave * 4 + i) * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(bb + b_off_g[i], (lds_void_t*)(base + BM * DMA_BK + (wave * 4 + i) * 1024),
+                                       16, 0, 0);
   };
 
   v4i acc[8][8];
@@ -335,50 +385,63 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
     a_off[i] = ra * DMA_BK + ((fchunk ^ ((ra >> 1) & 3)) * 16);
     b_off[i] = BM * DMA_BK + rb * DMA_BK + ((fchunk ^ ((rb >> 1) & 3)) * 16);
   }
-
   // Fragments are double-buffered in registers: while the MFMAs of step t run
-  // on fa/fb[t&1], the LDS reads of step t+1 fill the other set.
-  auto load_frags = [&](int t, v4i (&af)[8], v4i (&bf)[8]) {
-    const int8_t* st = &lds[t & (DMA_STAGES - 1)][0];
+  // on one set, the LDS reads of step t+1 fill the other.
+  auto load_frags = [&](int t, v4i (&af)[8], v4i (&bf)[8]) __attribute__((always_inline)) {
+    const int8_t* st = &lds[t % DMA_STAGES][0];
 #pragma unroll
     for (int j = 0; j < 8; ++j) bf[j] = *reinterpret_cast<const v4i*>(st + b_off[j]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) af[i] = *reinterpret_cast<const v4i*>(st + a_off[i]);
   };
-  v4i fa0[8], fb0[8], fa1[8], fb1[8];
-
-  const int ksteps = p.K / DMA_BK;
-  // prologue: stages 0..3 in flight, wait for stage 0, read its fragments
-#pragma unroll
-  for (int s = 0; s < DMA_STAGES; ++s)
-    if (s < ksteps) issue(s);
-  wait_vm(min(ksteps - 1, DMA_STAGES - 1));
-  asm volatile("s_barrier" ::: "memory");
-  load_frags(0, fa0, fb0);
-
-  // step t: [this wave's fragment reads of step t done] + [stage t+1 landed]
-  // -> barrier (every wave is past its reads of stage t, so its buffer can
-  // take stage t+4) -> refill -> MFMAs of step t with the reads of step t+1
-  // in flight underneath.
-  auto step = [&](int t, v4i (&af)[8], v4i (&bf)[8], v4i (&an)[8], v4i (&bn)[8]) {
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0), vmcnt/expcnt untouched
-    if (t + 1 < ksteps) wait_vm(min(ksteps - 2 - t, DMA_STAGES - 2));
-    asm volatile("s_barrier" ::: "memory");
-    if (t + DMA_STAGES < ksteps) issue(t + DMA_STAGES);
-    if (t + 1 < ksteps) load_frags(t + 1, an, bn);
+  auto mfmas = [&](v4i (&af)[8], v4i (&bf)[8]) __attribute__((always_inline)) {
     static_for<8>([&](auto I) {
       static_for<8>([&](auto J) {
         acc[I][J] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[J], af[I], acc[I][J], 0, 0, 0);
       });
     });
   };
-  int t = 0;
-  for (; t + 1 < ksteps; t += 2) {
+  v4i fa0[8], fb0[8], fa1[8], fb1[8];
+
+  // Every step has the same branch-free body, so the scheduler can interleave
+  // the DMA and the LDS reads with the MFMAs. In the last STAGES steps the DMA
+  // re-fetches the final K-slice into buffers that are never read again, and
+  // the last step's fragment reads fetch data that is never used; both stay in
+  // bounds. ksteps is even (host: K % 128 == 0), so the 2x unrolled loop has
+  // no tail.
+  const int ksteps = p.K / DMA_BK;
+#pragma unroll
+  for (int s = 0; s < DMA_STAGES; ++s) issue(min(s, ksteps - 1), s);
+  wait_vm_n<DMA_STAGES - 1>();
+  asm volatile("s_barrier" ::: "memory");
+  load_frags(0, fa0, fb0);
+
+  // Step t: [own fragment reads of step t done] + [own DMA of stage t+1
+  // landed] -> barrier (no wave reads stage t's buffer any more, so it takes
+  // stage t+STAGES) -> refill -> reads of step t+1 -> MFMAs of step t.
+  auto step = [&](int t, v4i (&af)[8], v4i (&bf)[8], v4i (&an)[8], v4i (&bn)[8]) __attribute__((always_inline)) {
+    wait_lgkm0();
+    wait_vm_n<DMA_STAGES - 2>();
+    asm volatile("s_barrier" ::: "memory");
+    issue(min(t + DMA_STAGES, ksteps - 1), t + DMA_STAGES);
+    load_frags(t + 1, an, bn);
+    mfmas(af, bf);
+#if XMH3_DMA_SCHED
+    static_for<8>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // one DMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two fragment reads
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // eight MFMAs
+    });
+#endif
+  };
+  for (int t = 0; t < ksteps; t += 2) {
     step(t, fa0, fb0, fa1, fb1);
     step(t + 1, fa1, fb1, fa0, fb0);
   }
-  if (t < ksteps) step(t, fa0, fb0, fa1, fb1);
-  epilogue<EPI, TO, VEC_OUT>(p, acc, m0, n0, wm, wn, lane);
+  wait_vm_n<0>();  // no DMA may land after the workgroup's LDS is released
+  EpiScales sc;
+  load_scales<EPI>(p, m0, n0, wm, wn, lane, sc);
+  epilogue<EPI, TO, VEC_OUT>(p, acc, sc, m0, n0, wm, wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -387,7 +450,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
 template <int BK, int EPI, typename TO>
 static int launch_gemm_T(GemmArgs& a, bool vec, hipStream_t st) {
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
-  if (a.K % DMA_BK == 0) {
+  const bool spans_ok = (int64_t)a.M * a.lda < (1LL << 31) && (int64_t)a.N * a.ldb < (1LL << 31);
+  if (a.K % (2 * DMA_BK) == 0 && spans_ok) {
     if (vec)
       hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
     else
