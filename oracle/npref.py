@@ -178,3 +178,50 @@ def w4_quantize(w: np.ndarray, group_size: int):
     u = (signed + 8).reshape(n, k)
     packed = ((u[:, 0::2] & 0xF) | ((u[:, 1::2] & 0xF) << 4)).astype(np.uint8).view(np.int8)
     return packed, s_rel, sch
+
+
+# ---------------------------------------------------------------------------
+# the reduction order of the reference's rms_norm (torch CPU sum)
+# ---------------------------------------------------------------------------
+
+def torch_cpu_sum_order(x: np.ndarray) -> np.float32:
+    """fp32 sum of a contiguous row in the order torch's CPU reduction uses for
+    it on this image: 8-lane vectors read 4 at a time into 4 accumulator rows
+    (32 chains, chain L over positions 32*i + L), each row accumulating in
+    chunks of 16 that feed a 4-level cascade (level 2 every 256 steps, level 3
+    every 4096), leftover vectors added to row 0, rows combined
+    ((r0+r1)+r2)+r3, then a scalar tail and the 8 lanes left to right."""
+    x = np.asarray(x, np.float32)
+    n = x.shape[0]
+    nvec = n // 8
+    vecs = x[: nvec * 8].reshape(nvec, 8)
+    size = nvec // 4
+    rows = vecs[: size * 4].reshape(size, 4, 8)
+    acc = np.zeros((4, 4, 8), np.float32)
+    i = 0
+    while i + 16 <= size:
+        for _ in range(16):
+            acc[0] = (acc[0] + rows[i]).astype(np.float32)
+            i += 1
+        for j in range(1, 4):
+            acc[j] = (acc[j] + acc[j - 1]).astype(np.float32)
+            acc[j - 1] = 0
+            if (i & (15 << (4 * j))) != 0:
+                break
+    while i < size:
+        acc[0] = (acc[0] + rows[i]).astype(np.float32)
+        i += 1
+    for j in range(1, 4):
+        acc[0] = (acc[0] + acc[j]).astype(np.float32)
+    part = acc[0]
+    for r in range(size * 4, nvec):
+        part[0] = (part[0] + vecs[r]).astype(np.float32)
+    p = part[0]
+    for k in range(1, 4):
+        p = (p + part[k]).astype(np.float32)
+    fin = np.float32(0)
+    for t in x[nvec * 8:]:
+        fin = np.float32(fin + t)
+    for v in range(8):
+        fin = np.float32(fin + p[v])
+    return fin

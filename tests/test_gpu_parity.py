@@ -143,6 +143,25 @@ def test_int8_linear_bit_exact(pkg, dev, out_dtype, per_channel, with_bias):
     assert same(y, yr, "int8_linear")
 
 
+def test_dequant_bf16_ties_round_to_even(pkg, dev):
+    """acc = n with unit scales: bf16 has 8 significant bits, so every odd
+    n in (256, 512) lies exactly halfway between two bf16 values; the epilogue
+    must round those ties to even like the reference's fp32 -> bf16 cast."""
+    say("dequant bf16 ties")
+    from x_minimaxh3_amd import backend
+
+    k = 512
+    a = torch.ones(4, k, dtype=torch.int8)
+    w = (torch.arange(k).view(1, -1) < torch.arange(k).view(-1, 1)).to(torch.int8)   # row n has n ones
+    one = torch.ones(1)
+    out = backend._gemm(a.to(dev), one.expand(4).contiguous().to(dev), w.to(dev), one.to(dev), None,
+                        torch.bfloat16)
+    torch.cuda.synchronize()
+    want = cpu_ref.dequant(cpu_ref.int8_mm(a, w), one.expand(4).reshape(-1, 1), one)
+    assert want[0, 257].item() == 256.0 and want[0, 259].item() == 260.0
+    assert same(out, want, "ties")
+
+
 def test_int8_linear_leading_dims_and_strided_input(pkg, dev):
     say("int8_linear 3D / strided")
     x = outlier_acts(2 * 65, 512, seed=4).reshape(2, 65, 512)
@@ -302,6 +321,7 @@ def test_norm_rope_720p(pkg, dev):
     for got, x, name in ((qo, nr["q"], "Q"), (ko, nr["k"], "K")):
         want = cpu_ref.norm_rope(x, nr["scale"], nr["shift"], nr["freqs"], 128, nr["eps"])
         close(got, want, f"norm_rope {name}")
+        assert same(got, want, f"norm_rope {name}")   # reference reduction order -> bit exact
 
 
 def test_rope_only_bit_exact(pkg, dev):
@@ -344,6 +364,7 @@ def test_h3_qknorm_rope_partial_inplace(pkg, dev):
     wk = cpu_ref.rms_rope_split_half1(qkv[:, :, 1], tab, kw, 1e-5, 96)
     close(out[:, :, 0], wq, "q")
     close(out[:, :, 1], wk, "k")
+    assert same(out[:, :, 0], wq, "q") and same(out[:, :, 1], wk, "k")
     assert torch.equal(out[:, :, 2], qkv[:, :, 2])    # v untouched
 
 
@@ -359,6 +380,7 @@ def test_rms_adaln(pkg, dev, mod_dtype):
     want = cpu_ref.rms_adaln(x, sc, sh, 1e-6)
     assert out.dtype == want.dtype
     close(out, want, "rms_adaln")
+    assert same(out, want, "rms_adaln")
 
 
 def test_h3_segmented_rms_adaln(pkg, dev):
@@ -373,4 +395,6 @@ def test_h3_segmented_rms_adaln(pkg, dev):
     segs = ((0, 77, 0), (77, 200, 1), (200, 1000, 2))
     out = h3.rms_adaln(x.to(dev), w.to(dev), sh.to(dev), sc.to(dev), segs, eps=1e-5)
     torch.cuda.synchronize()
-    close(out, cpu_ref.rms_adaln_segmented(x, w, sh, sc, segs, eps=1e-5), "segmented rms_adaln")
+    want = cpu_ref.rms_adaln_segmented(x, w, sh, sc, segs, eps=1e-5)
+    close(out, want, "segmented rms_adaln")
+    assert same(out, want, "segmented rms_adaln")

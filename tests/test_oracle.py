@@ -274,3 +274,19 @@ def test_segmented_adaln_matches_per_segment_rms_adaln():
     out = cpu_ref.rms_adaln_segmented(x, None, sh, sc, segs, eps=1e-5)
     for a, b, r in segs:
         assert torch.equal(out[a:b], cpu_ref.rms_adaln(x[a:b], sc[r:r + 1], sh[r:r + 1], 1e-5))
+
+
+@pytest.mark.parametrize("d", [5120, 5376, 128, 1000, 96, 16384, 13824, 72])
+def test_rms_norm_reduction_order_is_pinned(d):
+    """The GPU norms sum squares in the order torch's CPU reduction uses on this
+    image; the numpy restatement of that order must reproduce torch's sum (and
+    through it F.rms_norm) exactly, or the order claim is wrong."""
+    g = torch.Generator().manual_seed(d)
+    xb = (torch.randn(24, d, generator=g) * torch.rand(24, 1, generator=g) * 10).to(torch.bfloat16)
+    xf = xb.float()
+    sq = (xf * xf).numpy()
+    emu = np.array([npref.torch_cpu_sum_order(r) for r in sq])
+    assert np.array_equal(emu.view(np.uint32), xf.pow(2).sum(-1).numpy().view(np.uint32))
+    rr = (np.float32(1) / np.sqrt(((emu / np.float32(d)).astype(np.float32) + np.float32(1e-6)).astype(np.float32)))
+    out = torch.from_numpy((xf.numpy() * rr.astype(np.float32)[:, None]).astype(np.float32)).to(torch.bfloat16)
+    assert torch.equal(out, F.rms_norm(xb, (d,), eps=1e-6))

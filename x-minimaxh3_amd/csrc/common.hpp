@@ -24,12 +24,16 @@ enum Status : int { XMH3_OK = 0, XMH3_EINVAL = 1, XMH3_EHIP = 2, XMH3_EUNSUPPORT
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+// fp32 -> bf16, round to nearest even, on gfx950's v_cvt_pk_bf16_f32 (NaN stays
+// NaN; finite values round exactly as the integer formula
+// (u + 0x7fff + ((u >> 16) & 1)) >> 16 does).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2_t v = __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.0f) & 0xffffu; }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
@@ -38,13 +42,12 @@ __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to
 // mode is. Subnormal results come from one fp32 add: |f| + 0.5 places the fp16
 // subnormal ulp (2^-24) at the last fp32 mantissa bit.
 __device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  // branch-free (selects only), usable inside fully unrolled element loops
   const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
-  if (e == 0) {
-    const float v = (float)m * 5.9604644775390625e-08f;  // m * 2^-24, exact
-    return s ? -v : v;
-  }
-  if (e == 31) return __uint_as_float(s | 0x7f800000u | (m << 13));
-  return __uint_as_float(s | ((e + 112u) << 23) | (m << 13));
+  const float sub = __uint_as_float(s | __float_as_uint((float)m * 5.9604644775390625e-08f));  // m * 2^-24
+  const uint32_t infnan = s | 0x7f800000u | (m << 13);
+  const uint32_t nrm = s | ((e + 112u) << 23) | (m << 13);
+  return e == 0 ? sub : __uint_as_float(e == 31 ? infnan : nrm);
 }
 __device__ __forceinline__ uint32_t f32_to_f16(float ff) {
   // branch-free: all three cases are computed and selected, so the function
@@ -65,7 +68,14 @@ struct BF16T {
   static constexpr int code = DT_BF16;
   __device__ static float load(uint32_t b) { return bf16_to_f32(b); }
   __device__ static uint32_t store(float f) { return f32_to_bf16(f); }
-  __device__ static float round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+  __device__ static float round(float f) { return __uint_as_float(pack_bf16x2(f, 0.0f) << 16); }
+  // round two values at once (one v_cvt_pk_bf16_f32)
+  __device__ static void round2(float& a, float& b) {
+    const uint32_t w = pack_bf16x2(a, b);
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  }
+  __device__ static uint32_t store2(float a, float b) { return pack_bf16x2(a, b); }
   __device__ static float tiny() { return 1.17549435e-38f; }
 };
 struct F16T {
@@ -74,6 +84,8 @@ struct F16T {
   __device__ static float load(uint32_t b) { return f16_to_f32(b); }
   __device__ static uint32_t store(float f) { return f32_to_f16(f); }
   __device__ static float round(float f) { return f16_to_f32(f32_to_f16(f)); }
+  __device__ static void round2(float& a, float& b) { a = round(a); b = round(b); }
+  __device__ static uint32_t store2(float a, float b) { return f32_to_f16(a) | (f32_to_f16(b) << 16); }
   __device__ static float tiny() { return 6.103515625e-05f; }
 };
 struct F32T {
@@ -82,6 +94,7 @@ struct F32T {
   __device__ static float load(float f) { return f; }
   __device__ static float store(float f) { return f; }
   __device__ static float round(float f) { return f; }
+  __device__ static void round2(float&, float&) {}
   __device__ static float tiny() { return 1.17549435e-38f; }
 };
 

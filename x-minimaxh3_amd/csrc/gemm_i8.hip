@@ -90,10 +90,7 @@ __device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, i
 
 // 4 consecutive outputs -> one 8- or 16-byte store
 __device__ __forceinline__ void store4(uint16_t* p, const float* v, BF16T) {
-  uint2 w;
-  w.x = f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16);
-  w.y = f32_to_bf16(v[2]) | (f32_to_bf16(v[3]) << 16);
-  *reinterpret_cast<uint2*>(p) = w;
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 __device__ __forceinline__ void store4(uint16_t* p, const float* v, F16T) {
   uint2 w;

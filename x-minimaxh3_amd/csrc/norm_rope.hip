@@ -25,6 +25,7 @@
 // CK = backends/turbo/vendor/comfy_kitchen.
 #include "common.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace xmh3 {
@@ -117,19 +118,98 @@ struct RowArgs {
   float eps;
 };
 
-// ROPE: items are (8 at head offset i, 8 at i + head_dim/2), IPH per head;
-// otherwise items are 8 consecutive elements. NSTEP steps of 64 items.
+// ---------------------------------------------------------------------------
+// Sum of squares of a row in the reference's reduction order.
+//
+// The reference normalises with torch's F.rms_norm on the CPU: mean =
+// sum(x*x) / D, where the sum is ATen's vectorised cascade sum. For a
+// contiguous fp32 row it runs as 8-lane vectors read 4 at a time into 4
+// accumulator rows -- 32 independent chains, chain L summing the squares at
+// positions 32*i + L -- each chain adding in chunks of 16 that feed a 4-level
+// cascade (acc1 += chunk; every 256 steps acc2 += acc1; every 4096 acc3 +=
+// acc2), a remainder added from zero, the levels folded ((a0+a1)+a2)+a3, the
+// 4 rows added lane-wise ((r0+r1)+r2)+r3 and the 8 lanes left to right.
+// Reproducing that order makes the GPU rms bit-identical to the reference's.
+//
+// When D/8 is not a multiple of 4, the 1-3 leftover 8-lane vectors are added
+// to accumulator row 0 (chains 0..7) after the cascade, before the rows are
+// combined. The row is staged in a per-wave LDS buffer; chain L runs on lane L
+// for the even chunks and on lane L+32 for the odd ones. Requires D % 8 == 0
+// and D < 2^17 (cascade step 16).
+// ---------------------------------------------------------------------------
+template <typename TX>
+__device__ __forceinline__ float ref_order_sumsq(const typename TX::storage* row, int D, int lane) {
+  const int L = lane & 31, h = lane >> 5;
+  const int steps = D >> 5;
+  const int nchunks = steps >> 4;
+  float acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+  auto apply = [&](float c, int i_end) {
+    acc1 = acc1 + c;
+    if ((i_end & (15 << 4)) == 0) {
+      acc2 = acc2 + acc1;
+      acc1 = 0.0f;
+      if ((i_end & (15 << 8)) == 0) {
+        acc3 = acc3 + acc2;
+        acc2 = 0.0f;
+      }
+    }
+  };
+  for (int jj = 0; jj < nchunks; jj += 2) {
+    const int j = jj + h;
+    float c = 0.0f;
+    if (j < nchunks) {
+      const typename TX::storage* p = row + j * 512 + L;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float v = TX::load(p[u * 32]);
+        c = c + v * v;
+      }
+    }
+    const float c_odd = __shfl(c, L + 32, 64);
+    if (h == 0) {
+      apply(c, (jj + 1) * 16);
+      if (jj + 1 < nchunks) apply(c_odd, (jj + 2) * 16);
+    }
+  }
+  float acc0 = 0.0f;
+  for (int i = nchunks * 16; i < steps; ++i) {
+    const float v = TX::load(row[i * 32 + L]);
+    acc0 = acc0 + v * v;
+  }
+  float tot = ((acc0 + acc1) + acc2) + acc3;
+  for (int q = steps * 4; q < (D >> 3); ++q) {   // leftover vectors -> row 0
+    const float v = TX::load(row[q * 8 + (L & 7)]);
+    if (L < 8) tot = tot + v * v;
+  }
+  const int v8 = lane & 7;
+  const float r0 = __shfl(tot, v8, 64), r1 = __shfl(tot, v8 + 8, 64);
+  const float r2 = __shfl(tot, v8 + 16, 64), r3 = __shfl(tot, v8 + 24, 64);
+  const float pv = ((r0 + r1) + r2) + r3;
+  float fin = 0.0f;
+#pragma unroll
+  for (int v = 0; v < 8; ++v) fin = fin + __shfl(pv, v, 64);
+  return fin;
+}
+
+// Row-span kernel (one wave per token row; the rows of Q and K of a token in
+// the same wave). ROPE: items are (8 at head offset i, 8 at i + head_dim/2),
+// IPH per head; otherwise items are 8 consecutive elements; NSTEP steps of 64
+// items per row, all held in VGPRs (16-byte loads and stores). The rows are
+// also staged in LDS (WPB waves per block, two row buffers each) for the
+// reference-order reduction. D % 8 == 0.
 template <typename TX, typename TM, typename TF, bool ROPE, bool ADALN, bool WEIGHT, int IPH, int NSTEP>
-__global__ __launch_bounds__(256) void rowspan_kernel(RowArgs a) {
+__global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
   using TO = typename std::conditional<ADALN, typename Promote<TX, TM>::type, TX>::type;
-  constexpr int EPI = ROPE ? 16 : 8;                 // elements per item
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  using S = typename TX::storage;
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+  constexpr int EPI = ROPE ? 16 : 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + wave;
   if (row >= a.rows) return;
   const int64_t items = a.D / EPI;
   const int nt = a.x1 ? 2 : 1;
+  S* lrow = reinterpret_cast<S*>(dyn_lds) + (int64_t)wave * 2 * a.D;
 
-  // element offsets (within the row) of the item's two 8-groups
   auto item_off = [&](int64_t u, int64_t& o0, int64_t& o1) {
     if constexpr (ROPE) {
       const int64_t head = u / IPH;
@@ -142,8 +222,8 @@ __global__ __launch_bounds__(256) void rowspan_kernel(RowArgs a) {
     }
   };
 
+  // load every row of this token into registers and stage it in LDS
   V8<TX> v[2][NSTEP][ROPE ? 2 : 1];
-  float ss[2] = {0.0f, 0.0f};
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     if (t >= nt) break;
@@ -155,28 +235,28 @@ __global__ __launch_bounds__(256) void rowspan_kernel(RowArgs a) {
         int64_t o0, o1;
         item_off(u, o0, o1);
         ld8<TX>(xb, row * a.ldx + o0, v[t][s][0]);
-        if constexpr (ROPE) ld8<TX>(xb, row * a.ldx + o1, v[t][s][1]);
-#pragma unroll
-        for (int h = 0; h < (ROPE ? 2 : 1); ++h)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float f = g8<TX>(v[t][s][h], j);
-            ss[t] = fmaf(f, f, ss[t]);
-          }
+        st8<TX>(lrow + t * a.D, o0, v[t][s][0]);
+        if constexpr (ROPE) {
+          ld8<TX>(xb, row * a.ldx + o1, v[t][s][1]);
+          st8<TX>(lrow + t * a.D, o1, v[t][s][1]);
+        }
       }
     }
   }
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS stores done
+  __builtin_amdgcn_wave_barrier();
   float rr[2];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const float tot = wave_sum(ss[t]);
-    rr[t] = 1.0f / sqrtf(tot / (float)a.D + a.eps);
+    rr[t] = 1.0f;
+    if (t < nt) {
+      const float tot = ref_order_sumsq<TX>(lrow + t * a.D, (int)a.D, lane);
+      rr[t] = 1.0f / sqrtf(tot / (float)a.D + a.eps);
+    }
   }
 
   int64_t mrow = 0;
   if constexpr (ADALN) mrow = a.row_map ? (int64_t)a.row_map[row] : row / a.mod_group;
-
-  // the table row is the same for every head when IPH divides 64
   Tab8<TF> tab;
   const int64_t trow = a.freqs_row_stride ? row * a.freqs_row_stride : 0;
   bool tab_loaded = false;
@@ -189,11 +269,11 @@ __global__ __launch_bounds__(256) void rowspan_kernel(RowArgs a) {
     item_off(u, o0, o1);
     if constexpr (ROPE) {
       if (!tab_loaded || (64 % IPH) != 0) {
-        const int it = (int)(u % IPH);
-        load_tab8<TF>(a.freqs, trow + (int64_t)it * 8 * 4, tab);
+        load_tab8<TF>(a.freqs, trow + (int64_t)(u % IPH) * 8 * 4, tab);
         tab_loaded = true;
       }
     }
+    float y[2][ROPE ? 2 : 1][8];
 #pragma unroll
     for (int h = 0; h < (ROPE ? 2 : 1); ++h) {
       const int64_t col = h ? o1 : o0;
@@ -209,55 +289,60 @@ __global__ __launch_bounds__(256) void rowspan_kernel(RowArgs a) {
         ld8<TM>(a.scale, mrow * a.mod_ld + col, sv);
         ld8<TM>(a.shift, mrow * a.mod_ld + col, hv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          t8[j] = TM::round(1.0f + g8<TM>(sv, j));  // (1 + scale) in scale's dtype
+        for (int j = 0; j < 8; j += 2) {
+          t8[j] = 1.0f + g8<TM>(sv, j);          // (1 + scale) in scale's dtype
+          t8[j + 1] = 1.0f + g8<TM>(sv, j + 1);
+          TM::round2(t8[j], t8[j + 1]);
           sh8[j] = g8<TM>(hv, j);
+          sh8[j + 1] = g8<TM>(hv, j + 1);
         }
       }
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         if (t >= nt) break;
-        float y8[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float n = g8<TX>(v[t][s][h], j) * rr[t];
-          if constexpr (WEIGHT) n = n * w8[j];
-          n = TX::round(n);                           // rms_norm output in x's dtype
+        for (int j = 0; j < 8; j += 2) {
+          float n0 = g8<TX>(v[t][s][h], j) * rr[t], n1 = g8<TX>(v[t][s][h], j + 1) * rr[t];
+          if constexpr (WEIGHT) { n0 = n0 * w8[j]; n1 = n1 * w8[j + 1]; }
+          TX::round2(n0, n1);                      // rms_norm output in x's dtype
           if constexpr (ADALN) {
-            n = TO::round(n * t8[j]);
-            n = TO::round(n + sh8[j]);
+            n0 = n0 * t8[j]; n1 = n1 * t8[j + 1];
+            TO::round2(n0, n1);
+            n0 = n0 + sh8[j]; n1 = n1 + sh8[j + 1];
+            TO::round2(n0, n1);
           }
-          y8[j] = n;
-        }
-        if constexpr (ROPE) {
-          // the rotation needs both halves of the item: stage the modulated
-          // values in the row buffer (exact: the host enforces TO == TX here)
-          static_assert(!ROPE || std::is_same<TO, TX>::value, "rope path keeps x's dtype");
-#pragma unroll
-          for (int j = 0; j < 8; ++j) s8<TX>(v[t][s][h], j, y8[j]);
-        } else {
-          V8<TO> ov;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) s8<TO>(ov, j, y8[j]);
-          st8<TO>(t ? a.o1 : a.o0, row * a.ldo + col, ov);
+          y[t][h][j] = n0;
+          y[t][h][j + 1] = n1;
         }
       }
     }
-    if constexpr (ROPE) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if (t >= nt) break;
-        V8<TX> r0, r1;
+    for (int t = 0; t < 2; ++t) {
+      if (t >= nt) break;
+      if constexpr (ROPE) {
+        static_assert(std::is_same<TO, TX>::value, "rope path keeps x's dtype");
+        uint32_t w0[4], w1[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float y0, y1;
-          rotate_pair<TF, TX>(g8<TX>(v[t][s][0], j), g8<TX>(v[t][s][1], j), tab.f[j][0],
-                              tab.f[j][1], tab.f[j][2], tab.f[j][3], y0, y1);
-          s8<TX>(r0, j, y0);
-          s8<TX>(r1, j, y1);
+        for (int j = 0; j < 8; j += 2) {
+          float p0[2], p1[2];
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float a0 = TF::round(y[t][0][j + e]), a1 = TF::round(y[t][1][j + e]);
+            const float* f = tab.f[j + e];
+            p0[e] = TF::round(TF::round(f[0] * a0) + TF::round(f[1] * a1));
+            p1[e] = TF::round(TF::round(f[2] * a0) + TF::round(f[3] * a1));
+          }
+          w0[j >> 1] = TX::store2(p0[0], p0[1]);
+          w1[j >> 1] = TX::store2(p1[0], p1[1]);
         }
-        st8<TX>(t ? a.o1 : a.o0, row * a.ldo + o0, r0);
-        st8<TX>(t ? a.o1 : a.o0, row * a.ldo + o1, r1);
+        S* ob = static_cast<S*>(t ? a.o1 : a.o0) + row * a.ldo;
+        *reinterpret_cast<uint4*>(ob + o0) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+        *reinterpret_cast<uint4*>(ob + o1) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+      } else {
+        V8<TO> ov;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s8<TO>(ov, j, y[t][0][j]);
+        st8<TO>(t ? a.o1 : a.o0, row * a.ldo + o0, ov);
       }
     }
   }
@@ -301,22 +386,57 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
   const int64_t ooff = b * a.ob + s * a.os + h * a.oh;
 
   V8<TX> v0, v1;
-  float ss = 0.0f;
   if (is_pair || is_tail) {
     ld8<TX>(a.x, xoff + c0, v0);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) { const float f = g8<TX>(v0, j); ss = fmaf(f, f, ss); }
-    if (is_pair) {
-      ld8<TX>(a.x, xoff + c1, v1);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) { const float f = g8<TX>(v1, j); ss = fmaf(f, f, ss); }
-    }
+    if (is_pair) ld8<TX>(a.x, xoff + c1, v1);
   }
   float rr = 1.0f;
   if constexpr (NORM) {
+    // per-head sum of squares in the reference's order (see ref_order_sumsq):
+    // the head is staged in LDS, lane g of the group walks chains
+    // L = g, g + LPH, ... (32 chains, each over positions 32*i + L), then the
+    // chain totals are combined row-wise and lane by lane.
+    __shared__ __attribute__((aligned(16))) typename TX::storage heads[256 / LPH][16 * LPH];
+    typename TX::storage* hrow = heads[threadIdx.x / LPH];
+    if (is_pair || is_tail) {
+      st8<TX>(hrow, c0, v0);
+      if (is_pair) st8<TX>(hrow, c1, v1);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    constexpr int NCH = LPH >= 32 ? 1 : 32 / LPH;
+    const int D = (int)a.D, steps = D >> 5;
+    float tch[NCH];
 #pragma unroll
-    for (int o = 1; o < LPH; o <<= 1) ss += __shfl_xor(ss, o, 64);
-    rr = 1.0f / sqrtf(ss / (float)a.D + a.eps);
+    for (int c = 0; c < NCH; ++c) {
+      const int L = it + c * LPH;
+      float acc = 0.0f;
+      if (L < 32) {
+        for (int i = 0; i < steps; ++i) {
+          const float x = TX::load(hrow[i * 32 + L]);
+          acc = acc + x * x;
+        }
+        for (int q = steps * 4; q < (D >> 3); ++q) {  // leftover 8-lane vectors -> row 0
+          const float x = TX::load(hrow[q * 8 + (L & 7)]);
+          if (L < 8) acc = acc + x * x;
+        }
+      }
+      tch[c] = acc;
+    }
+    const int gbase = lane - (lane % LPH);
+    float fin = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      float rsum = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int L = v + 8 * r;
+        const float t = __shfl(tch[(L / LPH) < NCH ? (L / LPH) : 0], gbase + (L % LPH), 64);
+        rsum = r ? rsum + t : t;
+      }
+      fin = fin + rsum;
+    }
+    rr = 1.0f / sqrtf(fin / (float)a.D + a.eps);
   }
   if (!live || !(is_pair || is_tail)) return;
 
@@ -352,21 +472,35 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+template <typename TX, typename TM, typename TF, bool ROPE, bool ADALN, bool WEIGHT, int IPH, int N>
+static int launch_row_n(RowArgs& a, hipStream_t st) {
+  const size_t per_wave = 2 * (size_t)a.D * sizeof(typename TX::storage);
+  const int wpb = (int)std::min<size_t>(4, (160 * 1024) / per_wave);
+  if (a.D % 8 != 0 || a.D >= (1 << 17) || wpb < 1)
+    return fail(XMH3_EUNSUPPORTED, "row-span kernel: width must be a multiple of 8 and below 2^17");
+  auto kern = rowspan_exact_kernel<TX, TM, TF, ROPE, ADALN, WEIGHT, IPH, N>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
+        hipSuccess)
+      return fail(XMH3_EHIP, "row-span kernel: cannot raise the dynamic LDS limit");
+    attr_set = true;
+  }
+  dim3 grid((unsigned)((a.rows + wpb - 1) / wpb));
+  hipLaunchKernelGGL(kern, grid, dim3(64 * wpb), per_wave * wpb, st, a);
+  return check_launch("rowspan_exact_kernel");
+}
+
 template <typename TX, typename TM, typename TF, bool ROPE, bool ADALN, bool WEIGHT, int IPH>
 static int launch_row(RowArgs& a, hipStream_t st) {
   const int64_t items = a.D / (ROPE ? 16 : 8);
   const int64_t steps = (items + 63) / 64;
-  dim3 grid((unsigned)((a.rows + 3) / 4));
-#define XMH3_R(N)                                                                                  \
-  if (steps <= N) {                                                                                \
-    hipLaunchKernelGGL((rowspan_kernel<TX, TM, TF, ROPE, ADALN, WEIGHT, IPH, N>), grid, dim3(256), \
-                       0, st, a);                                                                  \
-    return check_launch("rowspan_kernel");                                                         \
-  }
+#define XMH3_R(N) \
+  if (steps <= N) return launch_row_n<TX, TM, TF, ROPE, ADALN, WEIGHT, IPH, N>(a, st);
   if constexpr (ROPE) {
-    XMH3_R(1) XMH3_R(2) XMH3_R(3) XMH3_R(4) XMH3_R(5) XMH3_R(6) XMH3_R(8)
+    XMH3_R(2) XMH3_R(4) XMH3_R(5) XMH3_R(8)
   } else {
-    XMH3_R(1) XMH3_R(2) XMH3_R(4) XMH3_R(6) XMH3_R(8) XMH3_R(10) XMH3_R(11) XMH3_R(12) XMH3_R(16)
+    XMH3_R(2) XMH3_R(4) XMH3_R(8) XMH3_R(11) XMH3_R(16)
   }
 #undef XMH3_R
   return fail(XMH3_EUNSUPPORTED, "row-span kernel: row too wide for the register path");
@@ -383,8 +517,7 @@ int norm_rope_rows(const void* x0, void* o0, const void* x1, void* o1, int dtype
   if (rows == 0) return XMH3_OK;
   XMH3_REQUIRE(x0 && o0 && freqs, "norm_rope: null pointer");
   XMH3_REQUIRE((x1 == nullptr) == (o1 == nullptr), "norm_rope: second tensor needs both in and out");
-  XMH3_REQUIRE(head_dim == 128 || head_dim == 64 || head_dim == 256,
-               "norm_rope: head_dim must be 64, 128 or 256");
+  XMH3_REQUIRE(head_dim == 128, "norm_rope: head_dim must be 128");
   XMH3_REQUIRE(D % head_dim == 0, "norm_rope: row width must be a multiple of head_dim");
   XMH3_REQUIRE(ldx % 8 == 0 && ldo % 8 == 0, "norm_rope: strides must be multiples of 8");
   XMH3_REQUIRE(dtype == mod_dtype || (scale == nullptr && shift == nullptr),
@@ -399,16 +532,10 @@ int norm_rope_rows(const void* x0, void* o0, const void* x1, void* o1, int dtype
   a.freqs = freqs; a.freqs_row_stride = freqs_row_stride; a.head_dim = head_dim; a.eps = eps;
   const bool adaln = scale != nullptr;
   XMH3_REQUIRE(adaln == (shift != nullptr), "norm_rope: scale and shift go together");
-#define XMH3_NR(TX, TF)                                                                          \
-  {                                                                                              \
-    if (adaln) {                                                                                 \
-      if (head_dim == 128) return launch_row<TX, TX, TF, true, true, false, 8>(a, st);           \
-      if (head_dim == 64) return launch_row<TX, TX, TF, true, true, false, 4>(a, st);            \
-      return launch_row<TX, TX, TF, true, true, false, 16>(a, st);                               \
-    }                                                                                            \
-    if (head_dim == 128) return launch_row<TX, TX, TF, true, false, false, 8>(a, st);            \
-    if (head_dim == 64) return launch_row<TX, TX, TF, true, false, false, 4>(a, st);             \
-    return launch_row<TX, TX, TF, true, false, false, 16>(a, st);                                \
+#define XMH3_NR(TX, TF)                                                         \
+  {                                                                             \
+    if (adaln) return launch_row<TX, TX, TF, true, true, false, 8>(a, st);      \
+    return launch_row<TX, TX, TF, true, false, false, 8>(a, st);                \
   }
   if (dtype == DT_BF16 && freqs_dtype == DT_F32) XMH3_NR(BF16T, F32T)
   if (dtype == DT_BF16 && freqs_dtype == DT_BF16) XMH3_NR(BF16T, BF16T)
@@ -481,7 +608,7 @@ int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, i
   const int items = rot / 16 + (int)(D - rot) / 8;
   int lph = 1;
   while (lph < items) lph <<= 1;
-  XMH3_REQUIRE(lph <= 64, "rope: head_dim too large");
+  XMH3_REQUIRE(lph <= 64 && D <= 512, "rope: head_dim must be at most 512");
   HeadArgs a{};
   a.x = x; a.out = out; a.B = B; a.S = S; a.H = H; a.D = D;
   a.sb = xstrides[0]; a.ss = xstrides[1]; a.sh = xstrides[2];
