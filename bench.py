@@ -34,6 +34,16 @@ sys.path.insert(0, str(ROOT))
 PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 
+# Bytes past L2 per launch of each kernel at these workloads, measured with
+# two rocprofv3 passes (--pmc FETCH_SIZE, then --pmc WRITE_SIZE) over
+# `bench.py --calibrate-copy`: a 1 GiB device copy reads 0.5 GiB by FETCH_SIZE
+# and 1 GiB by WRITE_SIZE, so FETCH_SIZE KiB are scaled x2 and WRITE_SIZE x1.
+TRAFFIC_BYTES = {
+    "fc1_gemm_gelu": (1432752.5 * 2 + 691031.8) * 1024,
+    "fc2_gemm": (1480923.4 * 2 + 252000.0) * 1024,
+    "norm_rope": (265271.7 * 2 + 504000.0) * 1024,
+}
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -85,6 +95,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-rows", type=int, default=2048)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run one 1 GiB device-to-device copy (reference for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the path shards along "
@@ -102,6 +114,14 @@ def main() -> int:
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(dev)
     log(f"device: {props.name} CUs={props.multi_processor_count}")
+
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("calibration copy: 1 GiB read + 1 GiB written")
 
     # ------------------------------------------------------------------ MLP
     cfg = workloads.CONFIGS["mlp_720p"]
@@ -212,16 +232,18 @@ def main() -> int:
                    "norm_rope_workload": "norm_rope_720p", "grid": [7, 45, 80], "heads": 40, "head_dim": 128},
         "frac_of_peak": round(tops / PEAK_INT8_TOPS, 4),
         "kernels_ms": {k: round(v, 4) for k, v in kavg.items()},
-        "roofline": {"kernel": "gemm_i8_kernel (fc1, dequant+GELU+row-amax epilogue)", "bound": "mfma",
+        "roofline": {"kernel": "gemm_i8_dma_kernel (fc1, dequant+GELU+row-amax epilogue)", "bound": "mfma",
                      "achieved": round(fc1_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                     "frac": round(fc1_tops / PEAK_INT8_TOPS, 4), "traffic": None,
-                     "algorithmic": "2*M*d*ffn int8 ops per launch"},
-        "roofline_fc2": {"kernel": "gemm_i8_kernel (fc2, dequant epilogue)", "bound": "mfma",
+                     "frac": round(fc1_tops / PEAK_INT8_TOPS, 4),
+                     "traffic": round(TRAFFIC_BYTES["fc1_gemm_gelu"]),
+                     "algorithmic": "2*M*d*ffn int8 ops per launch (unit: 1e12 int8 ops/s)"},
+        "roofline_fc2": {"kernel": "gemm_i8_dma_kernel (fc2, dequant epilogue)", "bound": "mfma",
                          "achieved": round(fc2_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
-                         "frac": round(fc2_tops / PEAK_INT8_TOPS, 4), "traffic": None},
-        "norm_rope": {"kernel": "rowspan_kernel (Q and K)", "bound": "hbm", "achieved": round(nr_gbs, 1),
+                         "frac": round(fc2_tops / PEAK_INT8_TOPS, 4),
+                         "traffic": round(TRAFFIC_BYTES["fc2_gemm"])},
+        "norm_rope": {"kernel": "rowspan_exact_kernel (Q and K)", "bound": "hbm", "achieved": round(nr_gbs, 1),
                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(nr_gbs / PEAK_HBM_GBS, 4),
-                      "us_per_launch": round(nr_ms * 1e3, 2), "traffic": None,
+                      "us_per_launch": round(nr_ms * 1e3, 2), "traffic": round(TRAFFIC_BYTES["norm_rope"]),
                       "algorithmic": "8*M*d bytes (Q,K read + written, bf16)"},
         "cpu_baseline": cpu,
         "cpu_baseline_norm_rope": cpu_nr,

@@ -129,7 +129,7 @@ int xmh3_w4a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, i
 /*
  * Fused AdaLN-modulated RMSNorm + split-half RoPE for Q and K of the same
  * tokens (k_in/k_out may be NULL): RMS over the full row of `width`, rotation
- * per head of head_dim (64, 128 or 256) with a table [tokens or 1,
+ * per head of head_dim (128) with a table [tokens or 1,
  * head_dim/2, 2, 2] of freqs_dtype (fp32 or x's dtype); scale/shift rows
  * [R, mod_ld] of x's dtype, token t uses row t / mod_group (NULL: no AdaLN).
  * In-place is allowed (q_out == q_in).
