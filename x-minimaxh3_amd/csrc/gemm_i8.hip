@@ -55,7 +55,7 @@ struct GemmArgs {
 };
 
 #ifndef XMH3_GROUP_M
-#define XMH3_GROUP_M 8
+#define XMH3_GROUP_M 4
 #endif
 #ifndef XMH3_NUM_XCD
 #define XMH3_NUM_XCD 8
@@ -442,12 +442,188 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// main loop v5 (K % 256 == 0): K-steps of 128 bytes, two LDS stages of
+// 64 KiB (A tile [256][128] at 0, B tile at 32 KiB), each DMA instruction
+// (buffer_load_dwordx4 ... lds) fetching 8 whole 128-byte rows, i.e. full
+// cache lines: with 64-byte row pieces the same bytes cost twice the L1/L2
+// transactions, and that request rate, not the MFMAs, set the loop's pace.
+// A 16-byte chunk c of row r sits in LDS slot c ^ (r & 7) (ds_read_b128
+// conflict-free). Each K-step runs as two 64-byte sub-steps whose fragments
+// are double-buffered in VGPRs: X holds the k0 half, Y the k1 half.
+//
+//   step t (stage t&1):
+//     sub 0: [X = (t, k0) ready]  read Y = (t, k1)       | MFMAs on X
+//     sub 1: [Y ready, slice t+1 landed] barrier -> DMA slice t+2 into stage
+//            t&1 (every wave has finished reading it) ; read X = (t+1, k0)
+//            from stage (t+1)&1                          | MFMAs on Y
+// A slice is therefore issued one full K-step (128 MFMAs per wave) before it
+// is first read. The DMA goes through a buffer resource based at the
+// workgroup's first row, so the K advance is a scalar offset; rows past M
+// or N are clamped to the last valid row (their products reach no stored
+// output).
+// ---------------------------------------------------------------------------
+constexpr int V5_BK = 128, V5_STAGE_BYTES = 2 * BM * V5_BK;
+
+// Raw buffer resource over [base, base + bytes): word 3 is the gfx9 data format
+// for untyped dword access.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt at their maximum (no wait on them)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int EPI, typename TO, bool VEC_OUT>
+__global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_v5_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) int8_t lds[2 * V5_STAGE_BYTES];
+
+  int tm, tn;
+  tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
+  const int lda = (int)p.lda, ldb = (int)p.ldb;
+  const __amdgpu_buffer_rsrc_t ra = raw_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)(rows_a * lda));
+  const __amdgpu_buffer_rsrc_t rb = raw_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)(rows_b * ldb));
+
+  // DMA: wave w fills 8-row blocks 8w + i (i < 8) of A and B; lane l fetches
+  // row 8*(8w+i) + l/8, chunk (l&7) ^ (row&7), landing at LDS byte 16*l of
+  // the block's 1 KiB.
+  uint32_t voa[8], vob[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = (wave * 8 + i) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ (r & 7);
+    voa[i] = (uint32_t)(min(r, rows_a - 1) * lda + c * 16);
+    vob[i] = (uint32_t)(min(r, rows_b - 1) * ldb + c * 16);
+  }
+  // DMA pair g (A and B block 8*wave + g) of K-slice kslice into stage STG
+  auto issue_pair = [&](int g, int kslice, auto STG) __attribute__((always_inline)) {
+    constexpr int s = decltype(STG)::value;
+    const int soff = kslice * V5_BK;
+    int8_t* base = lds + s * V5_STAGE_BYTES + wave * 8192 + g * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void_t*)base, 16, voa[g], soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void_t*)(base + BM * V5_BK), 16, vob[g], soff, 0, 0);
+  };
+  auto issue = [&](int kslice, auto STG) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) issue_pair(g, kslice, STG);
+  };
+
+  v4i acc[8][8];
+  static_for<8>([&](auto I) { static_for<8>([&](auto J) { acc[I][J] = v4i{0, 0, 0, 0}; }); });
+
+  // Fragment (i, half h): row wm*128 + 16 i + lane%16, logical chunk
+  // 4h + lane/16; the swizzle term row&7 = lane&7, so every fragment of a
+  // stage is one per-lane base plus a constant.
+  const int frow = lane & 15, fchunk = lane >> 4;
+  const int8_t* fa_base = lds + (wm * 128 + frow) * V5_BK;
+  const int8_t* fb_base = lds + BM * V5_BK + (wn * 128 + frow) * V5_BK;
+  const int sw0 = ((fchunk) ^ (frow & 7)) * 16, sw1 = ((4 + fchunk) ^ (frow & 7)) * 16;
+  auto load_pair = [&](auto STG, auto HALF, int g, v4i (&af)[8], v4i (&bf)[8]) __attribute__((always_inline)) {
+    constexpr int s = decltype(STG)::value;
+    constexpr int h = decltype(HALF)::value;
+    const int sw = h ? sw1 : sw0;
+    bf[g] = *reinterpret_cast<const v4i*>(fb_base + sw + s * V5_STAGE_BYTES + g * 16 * V5_BK);
+    af[g] = *reinterpret_cast<const v4i*>(fa_base + sw + s * V5_STAGE_BYTES + g * 16 * V5_BK);
+  };
+  auto load_frags = [&](auto STG, auto HALF, v4i (&af)[8], v4i (&bf)[8]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) load_pair(STG, HALF, g, af, bf);
+  };
+  // The MFMA is written as inline asm with the accumulator tied in place
+  // ("+a"): with the builtin, the register allocator rotates the 64
+  // accumulator tuples through copies on every pass of the pipelined loop.
+  // Hazards the compiler cannot see through the asm: the accumulators are
+  // written by VALU long before the first MFMA (prologue), and the epilogue
+  // reads them only after explicit wait states (below).
+  auto mfma_row = [&](auto I, v4i (&af)[8], v4i (&bf)[8]) __attribute__((always_inline)) {
+    static_for<8>([&](auto J) {
+      v4i& c = acc[I][J];
+      const v4i& xb = bf[J];
+      const v4i& xa = af[I];
+      asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(c) : "v"(xb), "v"(xa));
+    });
+  };
+  v4i xa[8], xb[8], ya[8], yb[8];
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
+
+  const int ksteps = p.K / V5_BK;  // even (host: K % 256 == 0)
+  issue(0, C0{});
+  issue(min(1, ksteps - 1), C1{});
+  wait_vmcnt<16>();
+  asm volatile("s_barrier" ::: "memory");
+  load_frags(C0{}, C0{}, xa, xb);
+
+  // Past the end the DMA re-fetches the last slice and the reads fetch unused
+  // data; both stay in bounds.
+  // The memory operations are spread over the MFMA stream in groups of 8
+  // MFMAs, pinned by scheduling barriers, so no burst of loads holds up MFMA
+  // issue. Two barriers per K-step: A (stage t&1 is read by nobody any more)
+  // early in sub-step 0, so the DMA of slice t+2 starts 1.5 K-steps before
+  // its first read; B (slice t+1 has landed in every wave) at sub-step 1.
+  // DMA pairs 0-5 go out in sub-step 0 after barrier A, pairs 6-7 in sub-step
+  // 1, so vmcnt <= 12 at B means slice t+1 is complete.
+  auto step = [&](int t, auto STG) __attribute__((always_inline)) {
+    constexpr int s = decltype(STG)::value;
+    const int knext = min(t + 2, ksteps - 1);
+    wait_lgkm0();                       // X = (t, k0) in registers
+    load_frags(STG, C1{}, ya, yb);      // Y = (t, k1): the last reads of stage s
+    mfma_row(C0{}, xa, xb);
+    mfma_row(C1{}, xa, xb);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_lgkm0();
+    asm volatile("s_barrier" ::: "memory");   // A
+    static_for<6>([&](auto G) {
+      issue_pair(G, knext, STG);
+      mfma_row(std::integral_constant<int, G + 2>{}, xa, xb);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    wait_vmcnt<12>();
+    asm volatile("s_barrier" ::: "memory");   // B
+    static_for<8>([&](auto G) {
+      if constexpr (G >= 6) issue_pair(G, knext, STG);
+      load_pair(std::integral_constant<int, s ^ 1>{}, C0{}, G, xa, xb);
+      mfma_row(G, ya, yb);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+  for (int t = 0; t < ksteps; t += 2) {
+    step(t, C0{});
+    step(t + 1, C1{});
+  }
+  // the last MFMA's result must be written back before VALU reads it
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  wait_vmcnt<0>();  // no DMA may land after the workgroup's LDS is released
+  EpiScales sc;
+  load_scales<EPI>(p, m0, n0, wm, wn, lane, sc);
+  epilogue<EPI, TO, VEC_OUT>(p, acc, sc, m0, n0, wm, wn, lane);
+}
+
+#ifndef XMH3_GEMM_KERNELS_ONLY
+// ---------------------------------------------------------------------------
 // host launcher
 // ---------------------------------------------------------------------------
 template <int BK, int EPI, typename TO>
 static int launch_gemm_T(GemmArgs& a, bool vec, hipStream_t st) {
   dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
   const bool spans_ok = (int64_t)a.M * a.lda < (1LL << 31) && (int64_t)a.N * a.ldb < (1LL << 31);
+#ifndef XMH3_GEMM_V5
+#define XMH3_GEMM_V5 1
+#endif
+  if (XMH3_GEMM_V5 && a.K % (2 * V5_BK) == 0 && spans_ok) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_i8_v5_kernel<EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
+    else
+      hipLaunchKernelGGL((gemm_i8_v5_kernel<EPI, TO, false>), grid, dim3(NTHREADS), 0, st, a);
+    return check_launch("gemm_i8_v5_kernel");
+  }
   if (a.K % (2 * DMA_BK) == 0 && spans_ok) {
     if (vec)
       hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
@@ -507,8 +683,10 @@ int int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_
   }
 }
 
+#endif  // XMH3_GEMM_KERNELS_ONLY
 }  // namespace xmh3
 
+#ifndef XMH3_GEMM_KERNELS_ONLY
 extern "C" int xmh3_int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_t M,
                               int64_t N, int64_t K, const float* sx, const float* sw,
                               int sw_per_channel, const void* bias, void* out, int out_dtype,
@@ -517,3 +695,4 @@ extern "C" int xmh3_int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int
   return xmh3::int8_gemm(A, lda, B, ldb, M, N, K, sx, sw, sw_per_channel, bias, out, out_dtype, ldo,
                          epilogue, row_absmax_bits, stream);
 }
+#endif
