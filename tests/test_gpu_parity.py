@@ -324,6 +324,57 @@ def test_norm_rope_720p(pkg, dev):
         assert same(got, want, f"norm_rope {name}")   # reference reduction order -> bit exact
 
 
+@pytest.mark.parametrize("d,m,with_k,tab_dtype,bcast", [
+    (5120, 37, True, torch.float32, False),     # pipelined kernel, fewer rows than waves
+    (5120, 1000, False, torch.float32, False),  # Q only
+    (3072, 1000, True, torch.bfloat16, False),  # bf16 table
+    (1024, 4099, True, torch.float32, True),    # one broadcast table row
+    (4096, 1, True, torch.float32, False),      # a single token
+    (1536, 300, True, torch.float32, False),    # width not a multiple of 1024 -> row kernel
+])
+def test_norm_rope_shapes(pkg, dev, d, m, with_k, tab_dtype, bcast):
+    say(f"norm_rope d={d} m={m} k={with_k} table={tab_dtype} broadcast={bcast}")
+    g = torch.Generator().manual_seed(d + m)
+    q = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    scale = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
+    shift = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
+    ang = torch.rand(1, 1 if bcast else m, 1, 64, generator=g) * 40
+    c, s = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -s, s, c), -1).reshape(1, ang.shape[1], 1, 64, 2, 2).to(tab_dtype)
+    from x_minimaxh3_amd import backend
+
+    qo, ko = backend.norm_rope(q.to(dev), k.to(dev) if with_k else None, scale.to(dev), shift.to(dev),
+                               tab.to(dev), 1e-6, 128)
+    torch.cuda.synchronize()
+    ftab = tab.expand(1, m, 1, 64, 2, 2)
+    outs = ((qo, q), (ko, k)) if with_k else ((qo, q),)
+    if not with_k:
+        assert ko is None
+    for got, x in outs:
+        want = cpu_ref.norm_rope(x, scale, shift, ftab, 128, 1e-6)
+        assert same(got, want, f"norm_rope d={d} m={m}")
+
+
+def test_norm_rope_per_sample_modulation(pkg, dev):
+    say("norm_rope with two modulation rows (two samples of 300 tokens)")
+    g = torch.Generator().manual_seed(5)
+    d, t = 5120, 300
+    q = torch.randn(2, t, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(2, t, d, generator=g).to(torch.bfloat16)
+    scale = (torch.randn(2, 1, d, generator=g) * 0.1).to(torch.bfloat16)
+    shift = (torch.randn(2, 1, d, generator=g) * 0.1).to(torch.bfloat16)
+    ang = torch.rand(1, 2 * t, 1, 64, generator=g) * 40
+    c, s = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -s, s, c), -1).reshape(1, 2 * t, 1, 64, 2, 2)
+    qo, ko = pkg.norm_rope(q.to(dev), k.to(dev), scale.to(dev), shift.to(dev), tab.to(dev), 1e-6, 128)
+    torch.cuda.synchronize()
+    for got, x in ((qo, q), (ko, k)):
+        for b in range(2):
+            want = cpu_ref.norm_rope(x[b], scale[b], shift[b], tab[:, b * t:(b + 1) * t], 128, 1e-6)
+            assert same(got[b], want, f"norm_rope sample {b}")
+
+
 def test_rope_only_bit_exact(pkg, dev):
     say("apply_rope_split_half fp32 + bf16 tables")
     g = torch.Generator().manual_seed(21)

@@ -462,8 +462,8 @@ def norm_rope(q: torch.Tensor, k: torch.Tensor | None, scale: torch.Tensor, shif
         k2, _, _, ldk = _aligned_rows(k)
         if ldk != ldq:
             q2, k2, ldq = q2.contiguous(), k2.contiguous(), width
-    sc, g1 = _modulation_rows(scale, q.reshape(m, width))
-    sh, g2 = _modulation_rows(shift, q.reshape(m, width))
+    sc, g1 = _modulation_rows(scale, q)
+    sh, g2 = _modulation_rows(shift, q)
     if g1 != g2:
         raise ValueError("scale and shift must broadcast the same way")
     f = freqs_cis

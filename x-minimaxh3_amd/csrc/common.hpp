@@ -68,12 +68,12 @@ struct BF16T {
   static constexpr int code = DT_BF16;
   __device__ static float load(uint32_t b) { return bf16_to_f32(b); }
   __device__ static uint32_t store(float f) { return f32_to_bf16(f); }
-  __device__ static float round(float f) { return __uint_as_float(pack_bf16x2(f, 0.0f) << 16); }
-  // round two values at once (one v_cvt_pk_bf16_f32)
+  // bf16(f) in the high half over a zero low half is the rounded value as an
+  // fp32 bit pattern: one v_cvt_pk_bf16_f32 with a zero first operand
+  __device__ static float round(float f) { return __uint_as_float(pack_bf16x2(0.0f, f)); }
   __device__ static void round2(float& a, float& b) {
-    const uint32_t w = pack_bf16x2(a, b);
-    a = __uint_as_float(w << 16);
-    b = __uint_as_float(w & 0xffff0000u);
+    a = round(a);
+    b = round(b);
   }
   __device__ static uint32_t store2(float a, float b) { return pack_bf16x2(a, b); }
   __device__ static float tiny() { return 1.17549435e-38f; }

@@ -21,7 +21,8 @@
 // x's dtype ((x*rrms)*w in fp32); 1+scale, the product and the sum each round
 // to the promoted dtype; the rotation's two products and their sum round to the
 // table's dtype, then the result rounds to x's dtype. No FMA contraction
-// (-ffp-contract=off); the only fused multiply-add is in the sum of squares.
+// (-ffp-contract=off); the only fused multiply-add is in the sum of squares of
+// 16-bit inputs, where the square is exact and fusing changes no bit.
 // CK = backends/turbo/vendor/comfy_kitchen.
 #include "common.hpp"
 
@@ -137,8 +138,22 @@ struct RowArgs {
 // for the even chunks and on lane L+32 for the odd ones. Requires D % 8 == 0
 // and D < 2^17 (cascade step 16).
 // ---------------------------------------------------------------------------
+// c + v*v. For 16-bit inputs v*v is exact in fp32, so the fused form rounds
+// identically to the reference's separate product and sum (one instruction
+// instead of two); fp32 inputs keep the separate rounding of the product.
 template <typename TX>
-__device__ __forceinline__ float ref_order_sumsq(const typename TX::storage* row, int D, int lane) {
+__device__ __forceinline__ float add_sq(float c, float v) {
+  if constexpr (sizeof(typename TX::storage) == 2) return __builtin_fmaf(v, v, c);
+  else return c + v * v;
+}
+
+struct IdentityIdx {
+  __device__ int operator()(int p) const { return p; }
+};
+
+template <typename TX, typename Idx = IdentityIdx>
+__device__ __forceinline__ float ref_order_sumsq(const typename TX::storage* row, int D, int lane,
+                                                 Idx idx = Idx{}) {
   const int L = lane & 31, h = lane >> 5;
   const int steps = D >> 5;
   const int nchunks = steps >> 4;
@@ -158,11 +173,10 @@ __device__ __forceinline__ float ref_order_sumsq(const typename TX::storage* row
     const int j = jj + h;
     float c = 0.0f;
     if (j < nchunks) {
-      const typename TX::storage* p = row + j * 512 + L;
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
-        const float v = TX::load(p[u * 32]);
-        c = c + v * v;
+        const float v = TX::load(row[idx(j * 512 + u * 32 + L)]);
+        c = add_sq<TX>(c, v);
       }
     }
     const float c_odd = __shfl(c, L + 32, 64);
@@ -173,13 +187,13 @@ __device__ __forceinline__ float ref_order_sumsq(const typename TX::storage* row
   }
   float acc0 = 0.0f;
   for (int i = nchunks * 16; i < steps; ++i) {
-    const float v = TX::load(row[i * 32 + L]);
-    acc0 = acc0 + v * v;
+    const float v = TX::load(row[idx(i * 32 + L)]);
+    acc0 = add_sq<TX>(acc0, v);
   }
   float tot = ((acc0 + acc1) + acc2) + acc3;
   for (int q = steps * 4; q < (D >> 3); ++q) {   // leftover vectors -> row 0
-    const float v = TX::load(row[q * 8 + (L & 7)]);
-    if (L < 8) tot = tot + v * v;
+    const float v = TX::load(row[idx(q * 8 + (L & 7))]);
+    if (L < 8) tot = add_sq<TX>(tot, v);
   }
   const int v8 = lane & 7;
   const float r0 = __shfl(tot, v8, 64), r1 = __shfl(tot, v8 + 8, 64);
@@ -349,6 +363,230 @@ __global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined norm-rope (single modulation row per launch).
+//
+// Persistent waves: wave w of the grid handles rows w, w + W, w + 2W, ... of
+// the (token, tensor) row list (row r = token * nt + tensor, nt = 1 or 2 for Q
+// only or Q and K), two rows ahead: while row i is reduced, normalised,
+// rotated and stored, the 16-byte loads of rows i+1 and i+2 are in flight in
+// two register buffers. A row's bytes land in the wave's LDS slice (row +
+// its RoPE table row) before the reduction, which runs in the reference's
+// order (ref_order_sumsq); the element pass then reads the row back from LDS.
+// The modulation (1 + scale rounded to the scale dtype, and shift) is the same
+// for every row, so the block turns it into fp32 once, in LDS, at start.
+// Nothing but the row and table loads goes through the vector-memory counter,
+// so waiting for row i never waits for anything issued later.
+//
+// LDS: WPB * (D * sizeof(x) + table row) + 2 * D * 4 bytes.
+// Items: u = s * 64 + lane (s < NSTEP), the 8 elements at head offset
+// 8 * (u % 8) and the 8 at +64 (head_dim 128, 8 items per head). Every lane
+// holds NSTEP items (D == 1024 * NSTEP): no predicated memory operation, so
+// the compiler's wait counts track both prefetched rows exactly.
+// ---------------------------------------------------------------------------
+// LDS placement of a staged row: element p of head h = p / 128 sits in half
+// ((p / 64) & 1) ^ flip(h) of the head's 256 bytes. flip alternates between
+// the heads one 64-lane access touches (8 consecutive heads for the 16-byte
+// items, heads 4 apart for the two lane halves of the ordered reduction), so
+// both kinds of access spread over all 64 banks.
+__device__ __forceinline__ int row_flip(int h) { return (h ^ (h >> 2)) & 1; }
+struct SwizzledRowIdx {
+  __device__ int operator()(int p) const {
+    const int h = p >> 7;
+    return (p & ~127) | ((((p >> 6) & 1) ^ row_flip(h)) << 6) | (p & 63);
+  }
+};
+
+template <typename TX, typename TF, bool ADALN, int NSTEP>
+__global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) {
+  using S = typename TX::storage;
+  using SF = typename TF::storage;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int HD = 128, IPH = HD / 16, TAB_ELEMS = HD / 2 * 4;
+  constexpr int TAB_CHUNKS = TAB_ELEMS * (int)sizeof(SF) / 16;   // 16-byte pieces of a table row
+  constexpr int EPC = 16 / (int)sizeof(SF);                      // table elements per piece
+  constexpr int CPG = TAB_CHUNKS / IPH;                          // pieces per 8-pair group
+  constexpr int D = NSTEP * 1024;
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpb = blockDim.x >> 6;
+  // modulation, lane-major: float4 (((s * 2 + half) * 2 + quad) * 64 + lane)
+  // holds columns col(s, half, lane) + 4 * quad .. + 3
+  f32x4* lt = reinterpret_cast<f32x4*>(dyn_lds);
+  f32x4* ls = lt + D / 4;
+  uint8_t* wbase = dyn_lds + (ADALN ? 8 * D : 0) + wave * (D * (int)sizeof(S) + TAB_ELEMS * (int)sizeof(SF));
+  S* lrow = reinterpret_cast<S*>(wbase);
+  u32x4* ltab = reinterpret_cast<u32x4*>(wbase + D * (int)sizeof(S));
+
+  if constexpr (ADALN) {
+    // t = round_TX(1 + scale), sh = shift, as fp32 (one modulation row)
+    const S* sc = static_cast<const S*>(a.scale);
+    const S* sh = static_cast<const S*>(a.shift);
+    for (int i = threadIdx.x; i < D / 4; i += blockDim.x) {
+      const int l = i & 63, q = (i >> 6) & 1, hf = (i >> 7) & 1, st = i >> 8;
+      const int u = st * 64 + l;
+      const int col = (u / IPH) * HD + hf * (HD / 2) + (u % IPH) * 8 + q * 4;
+      f32x4 tv, sv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        tv[e] = TX::round(1.0f + TX::load(sc[col + e]));
+        sv[e] = TX::load(sh[col + e]);
+      }
+      lt[i] = tv;
+      ls[i] = sv;
+    }
+    __syncthreads();
+  }
+
+  const int nrows = (int)a.rows * nt;
+  const int stride = gridDim.x * wpb;
+  const int tshift = nt - 1;            // token = row >> tshift, tensor = row & tshift
+  int r = blockIdx.x * wpb + wave;
+  if (r >= nrows) return;
+
+  // item slots of this lane in the staged row (the same for every row)
+  int off0[NSTEP], off1[NSTEP], slot0[NSTEP], slot1[NSTEP];
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const int u = s * 64 + lane;
+    const int head = u / IPH, it = u % IPH;
+    off0[s] = head * HD + it * 8;
+    off1[s] = off0[s] + HD / 2;
+    slot0[s] = head * HD + (row_flip(head) << 6) + it * 8;
+    slot1[s] = head * HD + ((row_flip(head) ^ 1) << 6) + it * 8;
+  }
+  const int tab_lane = min(lane, TAB_CHUNKS - 1);
+  // table piece c = tab_lane goes to slot (c % CPG) * 8 + c / CPG, so the
+  // lanes of one 8-pair group read consecutive slots
+  const int tab_slot = (tab_lane % CPG) * IPH + tab_lane / CPG;
+
+  // loads of one row into a buffer; past the last row the last row is
+  // re-read (never processed), so every wave issues the same sequence
+  auto issue = [&](int row, u32x4 (&bx)[NSTEP][2], u32x4& bt) __attribute__((always_inline)) {
+    row = row < nrows ? row : nrows - 1;
+    const int64_t tok = row >> tshift;
+    const S* xb = static_cast<const S*>((row & tshift) ? a.x1 : a.x0) + tok * a.ldx;
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+      bx[s][0] = *reinterpret_cast<const u32x4*>(xb + off0[s]);
+      bx[s][1] = *reinterpret_cast<const u32x4*>(xb + off1[s]);
+    }
+    const SF* tb = static_cast<const SF*>(a.freqs) + (a.freqs_row_stride ? tok * a.freqs_row_stride : 0);
+    bt = *reinterpret_cast<const u32x4*>(tb + tab_lane * EPC);
+  };
+
+  auto process = [&](int row, u32x4 (&bx)[NSTEP][2], u32x4& bt) __attribute__((always_inline)) {
+    // stage row + table in LDS
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+      *reinterpret_cast<u32x4*>(lrow + slot0[s]) = bx[s][0];
+      *reinterpret_cast<u32x4*>(lrow + slot1[s]) = bx[s][1];
+    }
+    if (lane < TAB_CHUNKS) ltab[tab_slot] = bt;
+    // the buffer is free again: loads of row i+2, kept in program order
+    // (ahead of this row's stores) so the next wait can leave them in flight
+    __builtin_amdgcn_sched_barrier(0);
+    issue(row + 2 * stride, bx, bt);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS stores done
+    __builtin_amdgcn_wave_barrier();
+    const float tot = ref_order_sumsq<TX>(lrow, D, lane, SwizzledRowIdx{});
+    const float rr = 1.0f / sqrtf(tot / (float)D + a.eps);
+    // this lane's 8 pairs (it * 8 .. it * 8 + 7) of the table row
+    Tab8<TF> tab;
+    {
+      SF el[CPG * EPC];
+#pragma unroll
+      for (int j = 0; j < CPG; ++j) {
+        const u32x4 v = ltab[j * IPH + (lane % IPH)];
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) {
+          if constexpr (sizeof(SF) == 4) el[j * EPC + e] = __uint_as_float(v[e]);
+          else el[j * EPC + e] = (SF)((v[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+        }
+      }
+#pragma unroll
+      for (int pp = 0; pp < 8; ++pp)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tab.f[pp][e] = TF::load(el[pp * 4 + e]);
+    }
+    const int64_t tok = row >> tshift;
+    S* ob = static_cast<S*>((row & tshift) ? a.o1 : a.o0) + tok * a.ldo;
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) {
+      float y[2][8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        V8<TX> xv;
+        xv.v = *reinterpret_cast<const uint4*>(lrow + (h ? slot1[s] : slot0[s]));
+        float t8[8], sh8[8];
+        if constexpr (ADALN) {
+          const int i0 = ((s * 2 + h) * 2) * 64 + lane;
+          const f32x4 ta = lt[i0], tb2 = lt[i0 + 64], sa = ls[i0], sb = ls[i0 + 64];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            t8[e] = ta[e]; t8[e + 4] = tb2[e];
+            sh8[e] = sa[e]; sh8[e + 4] = sb[e];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          float n0 = g8<TX>(xv, j) * rr, n1 = g8<TX>(xv, j + 1) * rr;
+          TX::round2(n0, n1);                      // rms_norm output in x's dtype
+          if constexpr (ADALN) {
+            n0 = n0 * t8[j]; n1 = n1 * t8[j + 1];
+            TX::round2(n0, n1);
+            n0 = n0 + sh8[j]; n1 = n1 + sh8[j + 1];
+            TX::round2(n0, n1);
+          }
+          y[h][j] = n0;
+          y[h][j + 1] = n1;
+        }
+      }
+      uint32_t w0[4], w1[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        float p0[2], p1[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float a0 = TF::round(y[0][j + e]), a1 = TF::round(y[1][j + e]);
+          const float* f = tab.f[j + e];
+          p0[e] = TF::round(TF::round(f[0] * a0) + TF::round(f[1] * a1));
+          p1[e] = TF::round(TF::round(f[2] * a0) + TF::round(f[3] * a1));
+        }
+        w0[j >> 1] = TX::store2(p0[0], p0[1]);
+        w1[j >> 1] = TX::store2(p1[0], p1[1]);
+      }
+      *reinterpret_cast<u32x4*>(ob + off0[s]) = u32x4{w0[0], w0[1], w0[2], w0[3]};
+      *reinterpret_cast<u32x4*>(ob + off1[s]) = u32x4{w1[0], w1[1], w1[2], w1[3]};
+    }
+    // the next row's staging overwrites this wave's LDS slice: every lane's
+    // reads of it must be done
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // The first row is peeled off the loop so that the loop is entered with the
+  // same memory operations outstanding as it has on its back edge; the
+  // compiler's wait counts then leave the second prefetched row in flight.
+  u32x4 x0[NSTEP][2], x1[NSTEP][2], t0, t1;
+  issue(r, x0, t0);
+  issue(r + stride, x1, t1);
+  __builtin_amdgcn_sched_barrier(0);
+  process(r, x0, t0);
+  r += stride;
+  while (r < nrows) {
+    process(r, x1, t1);
+    r += stride;
+    if (r >= nrows) break;
+    process(r, x0, t0);
+    r += stride;
+  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): no load lands after the wave ends
+}
+
+// ---------------------------------------------------------------------------
 // head-span kernel: LPH lanes per (b, s, h) head
 // ---------------------------------------------------------------------------
 struct HeadArgs {
@@ -414,11 +652,11 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
       if (L < 32) {
         for (int i = 0; i < steps; ++i) {
           const float x = TX::load(hrow[i * 32 + L]);
-          acc = acc + x * x;
+          acc = add_sq<TX>(acc, x);
         }
         for (int q = steps * 4; q < (D >> 3); ++q) {  // leftover 8-lane vectors -> row 0
           const float x = TX::load(hrow[q * 8 + (L & 7)]);
-          if (L < 8) acc = acc + x * x;
+          if (L < 8) acc = add_sq<TX>(acc, x);
         }
       }
       tch[c] = acc;
@@ -508,6 +746,61 @@ static int launch_row(RowArgs& a, hipStream_t st) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+constexpr size_t LDS_BYTES = 160 * 1024;   // gfx950 LDS per workgroup
+
+// Persistent launch of the pipelined norm-rope kernel. Returns -1 (no launch)
+// when the row does not fit the kernel's LDS plan.
+template <typename TX, typename TF, bool ADALN, int N>
+static int launch_pipe_n(RowArgs& a, int nt, hipStream_t st) {
+  const size_t per_wave = (size_t)a.D * sizeof(typename TX::storage) + 64 * 4 * sizeof(typename TF::storage);
+  const size_t mod = ADALN ? 8 * (size_t)a.D : 0;
+  if (mod + per_wave > LDS_BYTES) return -1;
+  const int wpb = (int)std::min<size_t>(8, (LDS_BYTES - mod) / per_wave);
+  const size_t lds = mod + (size_t)wpb * per_wave;
+  auto kern = norm_rope_pipe_kernel<TX, TF, ADALN, N>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES) !=
+        hipSuccess)
+      return fail(XMH3_EHIP, "norm-rope kernel: cannot raise the dynamic LDS limit");
+    attr_set = true;
+  }
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * wpb, lds) != hipSuccess || per_cu < 1)
+    per_cu = 1;
+  const int cus = std::max(1, cu_count());
+  const int64_t nrows = a.rows * nt;
+  const int64_t grid = std::min<int64_t>((nrows + wpb - 1) / wpb, (int64_t)cus * per_cu);
+  if (nrows + 2 * grid * wpb >= (1LL << 31)) return -1;   // the kernel counts rows in int32
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * wpb), lds, st, a, nt);
+  return check_launch("norm_rope_pipe_kernel");
+}
+
+template <typename TX, typename TF, bool ADALN>
+static int launch_pipe(RowArgs& a, int nt, hipStream_t st) {
+  if (a.D % 1024 != 0) return -1;
+  switch (a.D / 1024) {
+    case 1: return launch_pipe_n<TX, TF, ADALN, 1>(a, nt, st);
+    case 2: return launch_pipe_n<TX, TF, ADALN, 2>(a, nt, st);
+    case 3: return launch_pipe_n<TX, TF, ADALN, 3>(a, nt, st);
+    case 4: return launch_pipe_n<TX, TF, ADALN, 4>(a, nt, st);
+    case 5: return launch_pipe_n<TX, TF, ADALN, 5>(a, nt, st);
+    default: return -1;
+  }
+}
+
 int norm_rope_rows(const void* x0, void* o0, const void* x1, void* o1, int dtype, int64_t rows,
                    int64_t D, int64_t ldx, int64_t ldo, const void* scale, const void* shift,
                    int mod_dtype, int64_t mod_ld, int64_t mod_group, const void* freqs,
@@ -532,8 +825,18 @@ int norm_rope_rows(const void* x0, void* o0, const void* x1, void* o1, int dtype
   a.freqs = freqs; a.freqs_row_stride = freqs_row_stride; a.head_dim = head_dim; a.eps = eps;
   const bool adaln = scale != nullptr;
   XMH3_REQUIRE(adaln == (shift != nullptr), "norm_rope: scale and shift go together");
+  const size_t fsize = freqs_dtype == DT_F32 ? 4 : 2;
+  XMH3_REQUIRE((freqs_row_stride * (int64_t)fsize) % 16 == 0, "norm_rope: table rows must be 16-byte aligned");
+  // one modulation row for every token (or none): the pipelined kernel
+  const bool one_mod_row = !adaln || mod_group >= rows;
+  const int nt = x1 ? 2 : 1;
 #define XMH3_NR(TX, TF)                                                         \
   {                                                                             \
+    if (one_mod_row) {                                                          \
+      const int rc = adaln ? launch_pipe<TX, TF, true>(a, nt, st)               \
+                           : launch_pipe<TX, TF, false>(a, nt, st);             \
+      if (rc >= 0) return rc;                                                   \
+    }                                                                           \
     if (adaln) return launch_row<TX, TX, TF, true, true, false, 8>(a, st);      \
     return launch_row<TX, TX, TF, true, false, false, 8>(a, st);                \
   }
