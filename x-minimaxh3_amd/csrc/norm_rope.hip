@@ -445,17 +445,17 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
   int r = blockIdx.x * wpb + wave;
   if (r >= nrows) return;
 
-  // item slots of this lane in the staged row (the same for every row)
-  int off0[NSTEP], off1[NSTEP], slot0[NSTEP], slot1[NSTEP];
-#pragma unroll
-  for (int s = 0; s < NSTEP; ++s) {
-    const int u = s * 64 + lane;
-    const int head = u / IPH, it = u % IPH;
-    off0[s] = head * HD + it * 8;
-    off1[s] = off0[s] + HD / 2;
-    slot0[s] = head * HD + (row_flip(head) << 6) + it * 8;
-    slot1[s] = head * HD + ((row_flip(head) ^ 1) << 6) + it * 8;
-  }
+  // Item slots of this lane (the same for every row). Step s adds 8 heads
+  // (1024 elements) and leaves row_flip unchanged (it depends on the head's
+  // bits 0 and 2 only), so every slot is a per-lane base plus a constant.
+  const int qh = lane / IPH, it8 = (lane % IPH) * 8;
+  const int obase = qh * HD + it8;
+  const int sbase0 = qh * HD + (row_flip(qh) << 6) + it8;
+  const int sbase1 = qh * HD + ((row_flip(qh) ^ 1) << 6) + it8;
+  auto off0 = [&](int s) { return obase + s * 1024; };
+  auto off1 = [&](int s) { return obase + s * 1024 + HD / 2; };
+  auto slot0 = [&](int s) { return sbase0 + s * 1024; };
+  auto slot1 = [&](int s) { return sbase1 + s * 1024; };
   const int tab_lane = min(lane, TAB_CHUNKS - 1);
   // table piece c = tab_lane goes to slot (c % CPG) * 8 + c / CPG, so the
   // lanes of one 8-pair group read consecutive slots
@@ -468,9 +468,9 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
     const int64_t tok = row >> tshift;
     const S* xb = static_cast<const S*>((row & tshift) ? a.x1 : a.x0) + tok * a.ldx;
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-      bx[s][0] = *reinterpret_cast<const u32x4*>(xb + off0[s]);
-      bx[s][1] = *reinterpret_cast<const u32x4*>(xb + off1[s]);
+    for (int s = 0; s < NSTEP; ++s) {   // streamed once: non-temporal
+      bx[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + off0(s)));
+      bx[s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + off1(s)));
     }
     const SF* tb = static_cast<const SF*>(a.freqs) + (a.freqs_row_stride ? tok * a.freqs_row_stride : 0);
     bt = *reinterpret_cast<const u32x4*>(tb + tab_lane * EPC);
@@ -480,8 +480,8 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
     // stage row + table in LDS
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) {
-      *reinterpret_cast<u32x4*>(lrow + slot0[s]) = bx[s][0];
-      *reinterpret_cast<u32x4*>(lrow + slot1[s]) = bx[s][1];
+      *reinterpret_cast<u32x4*>(lrow + slot0(s)) = bx[s][0];
+      *reinterpret_cast<u32x4*>(lrow + slot1(s)) = bx[s][1];
     }
     if (lane < TAB_CHUNKS) ltab[tab_slot] = bt;
     // the buffer is free again: loads of row i+2, kept in program order
@@ -519,7 +519,7 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         V8<TX> xv;
-        xv.v = *reinterpret_cast<const uint4*>(lrow + (h ? slot1[s] : slot0[s]));
+        xv.v = *reinterpret_cast<const uint4*>(lrow + (h ? slot1(s) : slot0(s)));
         float t8[8], sh8[8];
         if constexpr (ADALN) {
           const int i0 = ((s * 2 + h) * 2) * 64 + lane;
@@ -558,8 +558,8 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
         w0[j >> 1] = TX::store2(p0[0], p0[1]);
         w1[j >> 1] = TX::store2(p1[0], p1[1]);
       }
-      *reinterpret_cast<u32x4*>(ob + off0[s]) = u32x4{w0[0], w0[1], w0[2], w0[3]};
-      *reinterpret_cast<u32x4*>(ob + off1[s]) = u32x4{w1[0], w1[1], w1[2], w1[3]};
+      __builtin_nontemporal_store(u32x4{w0[0], w0[1], w0[2], w0[3]}, reinterpret_cast<u32x4*>(ob + off0(s)));
+      __builtin_nontemporal_store(u32x4{w1[0], w1[1], w1[2], w1[3]}, reinterpret_cast<u32x4*>(ob + off1(s)));
     }
     // the next row's staging overwrites this wave's LDS slice: every lane's
     // reads of it must be done
