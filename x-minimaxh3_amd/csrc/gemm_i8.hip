@@ -102,50 +102,59 @@ __device__ __forceinline__ void store4(float* p, const float* v, F32T) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-// Epilogue shared by both main loops. Lane holds, for block (i, j): row
-// m = m0 + wm*128 + i*16 + lane%16, columns n = n0 + wn*128 + j*16 +
-// 4*(lane/16) + {0..3}. Straight-line code only (compile-time block indices,
-// guards as predicates) so the accumulators stay in registers.
-// Row and column scales of a wave's 128x128 sub-tile, all loaded in one batch
-// when the main loop ends (the fragment registers are free then), so the
-// epilogue pays one memory latency instead of one per output element (with one
-// wave per SIMD nothing else hides it).
-struct EpiScales {
-  float sx[8];      // rows m = em + 16 i
-  float sw[8][4];   // columns n = en + 16 j + r
+// Epilogue shared by the main loops. Lane holds, for accumulator block (i, j)
+// of a wave sub-tile at (row0, col0): row m = row0 + i*16 + lane%16, columns
+// n = col0 + j*16 + 4*(lane/16) + {0..3}. Straight-line code only
+// (compile-time block indices, guards as predicates) so the accumulators stay
+// in registers. The row and column scales of the sub-tile are all loaded in
+// one batch when the main loop ends (the fragment registers are free then), so
+// the epilogue pays one memory latency instead of one per output element.
+template <int NI = 8, int NJ = 8>
+struct EpiScalesT {
+  float sx[NI];      // rows m = em + 16 i
+  float sw[NJ][4];   // columns n = en + 16 j + r
 };
+using EpiScales = EpiScalesT<8, 8>;
+
+// (row0, col0): origin of the wave's NI*16 x NJ*16 sub-tile
+template <int EPI, int NI, int NJ>
+__device__ __forceinline__ void load_scales_t(const GemmArgs& p, int row0, int col0, int lane,
+                                              EpiScalesT<NI, NJ>& sc) {
+  // Branch-free: indices are clamped into range (rows and columns past the
+  // end are never stored), so every load is issued up front in one batch
+  // instead of being sunk into a conditional block next to its use.
+  if constexpr (EPI != EPI_INT32) {
+    const int em = row0 + (lane & 15);
+    const int en = col0 + 4 * (lane >> 4);
+    const int nmask = p.sw_per_channel ? -1 : 0;   // per-tensor scale: index 0
+#pragma unroll
+    for (int i = 0; i < NI; ++i) sc.sx[i] = p.sx[min(em + i * 16, p.M - 1)];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc.sw[j][r] = p.sw[min(en + j * 16 + r, p.N - 1) & nmask];
+  }
+}
 
 template <int EPI>
 __device__ __forceinline__ void load_scales(const GemmArgs& p, int m0, int n0, int wm, int wn, int lane,
                                             EpiScales& sc) {
-  if constexpr (EPI != EPI_INT32) {
-    const int em = m0 + wm * 128 + (lane & 15);
-    const int en = n0 + wn * 128 + 4 * (lane >> 4);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) sc.sx[i] = (em + i * 16 < p.M) ? p.sx[em + i * 16] : 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = en + j * 16 + r;
-        sc.sw[j][r] = p.sw_per_channel ? (n < p.N ? p.sw[n] : 0.0f) : p.sw[0];
-      }
-  }
+  load_scales_t<EPI, 8, 8>(p, m0 + wm * 128, n0 + wn * 128, lane, sc);
 }
 
-template <int EPI, typename TO, bool VEC_OUT>
-__device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], const EpiScales& sc, int m0,
-                                         int n0, int wm, int wn, int lane) {
-  const int em = m0 + wm * 128 + (lane & 15);
-  const int en = n0 + wn * 128 + 4 * (lane >> 4);
-  static_for<8>([&](auto I) {
+template <int EPI, typename TO, bool VEC_OUT, bool BIAS, int NI, int NJ>
+__device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][NJ], const EpiScalesT<NI, NJ>& sc,
+                                              int row0, int col0, int lane) {
+  const int em = row0 + (lane & 15);
+  const int en = col0 + 4 * (lane >> 4);
+  static_for<NI>([&](auto I) {
     constexpr int i = I;
     const int m = em + i * 16;
     const bool mok = m < p.M;
     float amax = 0.0f;
     float sxm = 0.0f;
     if constexpr (EPI != EPI_INT32) sxm = sc.sx[i];
-    static_for<8>([&](auto J) {
+    static_for<NJ>([&](auto J) {
       constexpr int j = J;
       const int n = en + j * 16;
       if constexpr (EPI == EPI_INT32) {
@@ -167,7 +176,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], co
         for (int r = 0; r < 4; ++r) {
           const bool nok = n + r < p.N;
           float y = TO::round((float)acc[i][j][r] * (sxm * sc.sw[j][r]));
-          if (brow) y = TO::round(y + (nok ? TO::load(brow[n + r]) : 0.0f));
+          if constexpr (BIAS) y = TO::round(y + TO::load(brow[min(n + r, p.N - 1)]));
           if constexpr (EPI == EPI_GELU) {
             y = TO::round(gelu_tanh_f32(y));
             amax = fmaxf(amax, nok ? fabsf(y) : 0.0f);
@@ -191,6 +200,23 @@ __device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], co
       if (lane < 16 && mok) atomicMax(p.row_amax + m, __float_as_uint(amax));
     }
   });
+}
+
+// The bias test is hoisted out of the element loop (a uniform branch per
+// element otherwise).
+template <int EPI, typename TO, bool VEC_OUT, int NI, int NJ>
+__device__ __forceinline__ void epilogue_t(const GemmArgs& p, v4i (&acc)[NI][NJ], const EpiScalesT<NI, NJ>& sc,
+                                           int row0, int col0, int lane) {
+  if (EPI != EPI_INT32 && p.bias)
+    epilogue_body<EPI, TO, VEC_OUT, true, NI, NJ>(p, acc, sc, row0, col0, lane);
+  else
+    epilogue_body<EPI, TO, VEC_OUT, false, NI, NJ>(p, acc, sc, row0, col0, lane);
+}
+
+template <int EPI, typename TO, bool VEC_OUT>
+__device__ __forceinline__ void epilogue(const GemmArgs& p, v4i (&acc)[8][8], const EpiScales& sc, int m0,
+                                         int n0, int wm, int wn, int lane) {
+  epilogue_t<EPI, TO, VEC_OUT, 8, 8>(p, acc, sc, m0 + wm * 128, n0 + wn * 128, lane);
 }
 
 template <int BK, int EPI, typename TO, bool VEC_OUT>

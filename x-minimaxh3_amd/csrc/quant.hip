@@ -17,6 +17,8 @@
 // A block-per-row two-pass kernel covers rows wider than the register path.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace xmh3 {
 
 // 8 elements of T as raw storage
@@ -64,6 +66,26 @@ __device__ __forceinline__ int quant_code_T(float x, float sT) {
   return (int)r;
 }
 
+// The same code from a reciprocal, for bf16: r = x * fl(1/sT). With x and sT
+// both bf16 (8 significant bits), x/sT is never within 2^-17 (relative) of a
+// bf16 rounding midpoint: a midpoint has an odd 9-bit significand, so
+// x = midpoint * sT would need at least 9 significant bits, and a quotient
+// that is not a midpoint differs from one by at least 1/(256 * 2^9) of it. r is
+// within 2^-23 (relative) of x/sT (two roundings of 2^-24; 1/sT stays normal
+// since sT <= 2^121 for finite bf16 rows), so bf16(r) == bf16(fl(x/sT)) and
+// the codes are identical. fp16 and fp32 keep the correctly rounded division.
+template <typename T>
+__device__ __forceinline__ int quant_code_rcp(float x, float sT, float inv) {
+  if constexpr (std::is_same<T, BF16T>::value) {
+    float v = T::round(x * inv);
+    float q = rintf(v);
+    q = fminf(fmaxf(q, -128.0f), 127.0f);
+    return (int)q;
+  } else {
+    return quant_code_T<T>(x, sT);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ float scale_for_math(float scale) {
   float sT = T::round(scale);
@@ -108,6 +130,7 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(
   amax = wave_max(amax);
   const float s = row_scale(amax);
   const float sT = scale_for_math<T>(s);
+  const float inv = 1.0f / sT;
   int8_t* qr = q + row * ldq;
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
@@ -115,9 +138,10 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(
     if (col < K) {
       uint32_t lo = 0, hi = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_T<T>(get8<T>(buf[i], j), sT) & 0xff) << (8 * j);
+      for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_rcp<T>(get8<T>(buf[i], j), sT, inv) & 0xff) << (8 * j);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= (uint32_t)(quant_code_T<T>(get8<T>(buf[i], j + 4), sT) & 0xff) << (8 * j);
+      for (int j = 0; j < 4; ++j)
+        hi |= (uint32_t)(quant_code_rcp<T>(get8<T>(buf[i], j + 4), sT, inv) & 0xff) << (8 * j);
       *reinterpret_cast<uint2*>(qr + col) = make_uint2(lo, hi);
     }
   }
@@ -165,30 +189,46 @@ __global__ __launch_bounds__(256) void quant_rows_generic_kernel(
 
 // ---------------------------------------------------------------------------
 // requant with a precomputed row amax (bit pattern of the bf16 |g| maximum,
-// produced by the fused fc1 epilogue): a pure streaming pass, 8 elements per
-// thread, 16-byte loads and 8-byte stores.
+// produced by the fused fc1 epilogue): a pure streaming pass, one wave per
+// row (the scale is computed once), 16-byte non-temporal loads of 8 values
+// and 8-byte stores of their codes, UNR chunks in flight per lane.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, int UNR>
 __global__ __launch_bounds__(256) void requant_rows_kernel(
     const typename T::storage* __restrict__ g, int64_t ldg, int64_t M, int64_t K,
     const uint32_t* __restrict__ row_amax, int8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale) {
-  const int64_t per_row = K >> 3;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= M * per_row) return;
-  const int64_t row = idx / per_row;
-  const int64_t col = (idx - row * per_row) << 3;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
   const float s = row_scale(__uint_as_float(row_amax[row]));
   const float sT = scale_for_math<T>(s);
-  Pack8<T> b;
-  load8<T>(g + row * ldg + col, b);
-  uint32_t lo = 0, hi = 0;
+  const float inv = 1.0f / sT;
+  const typename T::storage* gr = g + row * ldg;
+  int8_t* qr = q + row * ldq;
+  const int chunks = (int)(K >> 3);
+  for (int c0 = 0; c0 < chunks; c0 += 64 * UNR) {
+    Pack8<T> b[UNR];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_T<T>(get8<T>(b, j), sT) & 0xff) << (8 * j);
+    for (int u = 0; u < UNR; ++u) {
+      const int c = min(c0 + u * 64 + lane, chunks - 1);
+      const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(gr + (int64_t)c * 8));
+      b[u].v = make_uint4(v.x, v.y, v.z, v.w);
+    }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) hi |= (uint32_t)(quant_code_T<T>(get8<T>(b, j + 4), sT) & 0xff) << (8 * j);
-  *reinterpret_cast<uint2*>(q + row * ldq + col) = make_uint2(lo, hi);
-  if (col == 0) scale[row] = s;
+    for (int u = 0; u < UNR; ++u) {
+      const int c = c0 + u * 64 + lane;
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_rcp<T>(get8<T>(b[u], j), sT, inv) & 0xff) << (8 * j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        hi |= (uint32_t)(quant_code_rcp<T>(get8<T>(b[u], j + 4), sT, inv) & 0xff) << (8 * j);
+      if (c < chunks) *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = make_uint2(lo, hi);
+    }
+  }
+  if (lane == 0) scale[row] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -249,13 +289,14 @@ int requant_rows(const void* g, int g_dtype, int64_t M, int64_t K, int64_t ldg,
   if (M == 0 || K == 0) return XMH3_OK;
   XMH3_REQUIRE(K % 8 == 0 && ldg % 8 == 0 && ldq % 8 == 0, "requant: K and strides must be multiples of 8");
   XMH3_REQUIRE(g_dtype == DT_BF16 || g_dtype == DT_F16, "requant: dtype must be bf16 or fp16");
-  const int64_t threads = M * (K / 8);
-  dim3 grid((unsigned)((threads + 255) / 256));
+  XMH3_REQUIRE(K / 8 < (1LL << 30), "requant: rows too wide");
+  XMH3_REQUIRE((uintptr_t)g % 16 == 0 && (uintptr_t)q % 8 == 0, "requant: misaligned pointers");
+  dim3 grid((unsigned)((M + 3) / 4));
   if (g_dtype == DT_BF16)
-    hipLaunchKernelGGL(requant_rows_kernel<BF16T>, grid, dim3(256), 0, st,
+    hipLaunchKernelGGL((requant_rows_kernel<BF16T, 4>), grid, dim3(256), 0, st,
                        static_cast<const uint16_t*>(g), ldg, M, K, row_amax, q, ldq, scale);
   else
-    hipLaunchKernelGGL(requant_rows_kernel<F16T>, grid, dim3(256), 0, st,
+    hipLaunchKernelGGL((requant_rows_kernel<F16T, 4>), grid, dim3(256), 0, st,
                        static_cast<const uint16_t*>(g), ldg, M, K, row_amax, q, ldq, scale);
   return check_launch("requant_rows_kernel");
 }
