@@ -1,21 +1,26 @@
 """Benchmark of the quantized DiT-block hot path on one MI355X.
 
-Workloads (synthetic, seeded, generated on the CPU then resident in HBM):
+Workloads (synthetic, seeded; inputs resident in HBM when the timed region
+starts):
   * W8A8 MLP at the 720p shape: M=25200 tokens, 5120 -> 13824 -> 5120,
     y = fc2(gelu_tanh(fc1(x))) with per-token int8 activations -- `value`
     (whole-job int8 TOPS, 4*M*d*ffn ops per step, quant/GELU/requant time
     included);
   * fused AdaLN-RMSNorm + 3D RoPE of Q and K at M=25200, d=5120 (40 x 128),
-    reported as HBM GB/s on 8*M*d algorithmic bytes.
+    reported as HBM GB/s on 8*M*d algorithmic bytes;
+  * W4A8 MLP at the same shape (group-128 int4 weights decoded on the GPU);
+  * the long 16x68x120 grid (M=130560): norm-rope + W8A8 MLP in 16384-token
+    chunks, HBM-resident (compute rate) and streamed from pinned host memory
+    through double-buffered device slots (end-to-end, PCIe included).
 
 A step is one pass of the MLP block over the batch. The timed region runs the
 four MLP kernels (per-token quant, fc1 GEMM + dequant/GELU/row-amax epilogue,
 requant, fc2 GEMM + dequant) through the C ABI on torch's current stream, with
-HIP events between them, so per-kernel durations come from the same region.
-The CPU baseline is the oracle (torch-CPU restatement of the reference's eager
-path) on a bounded row sample, run on this host's cores.
+HIP events between them on that stream, so per-kernel durations come from the
+same region. The CPU baseline is the oracle (torch-CPU restatement of the
+reference's eager path) on a bounded row sample, run on this host's cores.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-extra]
 """
 
 from __future__ import annotations
@@ -34,10 +39,11 @@ sys.path.insert(0, str(ROOT))
 PEAK_INT8_TOPS = 5000.0      # MI355X dense int8 MFMA, 5.0 POP/s
 PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 
-# Bytes past L2 per launch of each kernel at these workloads, measured with
-# two rocprofv3 passes (--pmc FETCH_SIZE, then --pmc WRITE_SIZE) over
-# `bench.py --calibrate-copy`: a 1 GiB device copy reads 0.5 GiB by FETCH_SIZE
-# and 1 GiB by WRITE_SIZE, so FETCH_SIZE KiB are scaled x2 and WRITE_SIZE x1.
+# HBM bytes per launch at these workloads, from two rocprofv3 passes
+# (--pmc FETCH_SIZE, then --pmc WRITE_SIZE, KiB per dispatch) over
+# `bench.py --calibrate-copy`; the 1 GiB device copy of that run reads
+# 0.5 GiB by FETCH_SIZE and 1 GiB by WRITE_SIZE, so FETCH_SIZE is scaled x2 and
+# WRITE_SIZE x1 (see profiles/).
 TRAFFIC_BYTES = {
     "fc1_gemm_gelu": (1432752.5 * 2 + 691031.8) * 1024,
     "fc2_gemm": (1480923.4 * 2 + 252000.0) * 1024,
@@ -88,12 +94,103 @@ def cpu_baseline_norm_rope(nr: dict, repeats: int = 3) -> dict:
             "kind": "port", "sample": f"oracle norm_rope on Q and K, full {m}x{d}, median of {repeats}"}
 
 
+def timed(fn, steps: int, warmup: int) -> float:
+    """Median ms of `fn` over `steps` launches, HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
+        fn()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    return statistics.median(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+
+
+def bench_w4a8(pkg, dev, steps: int, warmup: int) -> dict:
+    import torch
+
+    from x_minimaxh3_amd import backend, workloads
+
+    cfg = workloads.CONFIGS["mlp_720p"]
+    g = torch.Generator(device=dev).manual_seed(1)
+    m, d, f = cfg["M"], cfg["d"], cfg["ffn"]
+    # weights from the reference's symmetric group-128 generator on the CPU
+    # (fp32 N(0, 0.02)), activations drawn on the GPU
+    gc = torch.Generator().manual_seed(1)
+    w1p, w1s, w1c = workloads.quantize_weight_w4(torch.randn(f, d, generator=gc) * 0.02, 128)
+    w2p, w2s, w2c = workloads.quantize_weight_w4(torch.randn(d, f, generator=gc) * 0.02, 128)
+    w = [t.to(dev) for t in (w1p, w1s, w1c, w2p, w2s, w2c)]
+    x = torch.randn(m, d, device=dev, generator=g).bfloat16()
+    out = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(pkg._lib.query("xmh3_w4a8_mlp_workspace_bytes", m, d, f), dtype=torch.uint8, device=dev)
+    ms = timed(lambda: backend.w4a8_mlp(x, *w, 128, out=out, workspace=ws), steps, warmup)
+    tops = 4.0 * m * d * f / (ms * 1e-3) / 1e12
+    return {"workload": "w4a8_mlp_720p", "tokens": m, "group_size": 128, "ms_per_step": round(ms, 4),
+            "value": round(tops, 2), "unit": "TOPS", "frac_of_peak": round(tops / PEAK_INT8_TOPS, 4),
+            "note": "both int4 weights decoded to the int8 grid on the GPU inside every step"}
+
+
+def bench_long(pkg, dev, inp: dict, warmup: int) -> dict:
+    import torch
+
+    from x_minimaxh3_amd import driver, workloads
+
+    cfg = workloads.CONFIGS["long_16x68x120"]
+    grid = cfg["grid"]
+    m, d, f, chunk = grid[0] * grid[1] * grid[2], cfg["d"], cfg["ffn"], cfg["chunk"]
+    g = torch.Generator(device=dev).manual_seed(2)
+    # activations drawn on the GPU with the same distributions as the 720p
+    # workloads (x with 51 outlier channels x20; Q, K N(0,1)); weights and
+    # modulation of the 720p run
+    x = torch.randn(m, d, device=dev, generator=g)
+    x[:, inp["outliers"].to(dev)] *= 20.0
+    x = x.bfloat16()
+    q = torch.randn(m, d, device=dev, generator=g).bfloat16()
+    k = torch.randn(m, d, device=dev, generator=g).bfloat16()
+    freqs = workloads.rope_table_3d(grid).to(dev)
+    scale = (torch.randn(1, d, device=dev, generator=g) * 0.1).bfloat16()
+    shift = (torch.randn(1, d, device=dev, generator=g) * 0.1).bfloat16()
+    w1, s1, w2, s2 = (inp[k_].to(dev) for k_ in ("w1", "s1", "w2", "s2"))
+    drv = driver.LongBlockDriver(w1, s1, w2, s2, scale, shift, chunk=chunk)
+    qo, ko, y = torch.empty_like(q), torch.empty_like(k), torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    ms_res = timed(lambda: drv.run_resident(q, k, x, freqs, qo, ko, y), 3, max(1, warmup // 2))
+    # streamed: the same tensors in pinned host memory
+    host = {n: torch.empty(m, d, dtype=torch.bfloat16, pin_memory=True) for n in ("q", "k", "x", "qo", "ko", "y")}
+    host["q"].copy_(q)
+    host["k"].copy_(k)
+    host["x"].copy_(x)
+    run = lambda: drv.run_streamed(host["q"], host["k"], host["x"], freqs, host["qo"], host["ko"], host["y"])
+    run()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    ms_str = statistics.median(times) * 1e3
+    same = bool(torch.equal(host["y"][:4096].to(dev), y[:4096]) and torch.equal(host["qo"][-4096:].to(dev), qo[-4096:]))
+    mlp_ops = 4.0 * m * d * f
+    moved = 6.0 * m * d * 2
+    return {"workload": "long_16x68x120", "tokens": m, "chunk": chunk,
+            "resident_ms": round(ms_res, 3), "resident_mlp_tops": round(mlp_ops / (ms_res * 1e-3) / 1e12, 2),
+            "streamed_ms": round(ms_str, 3), "streamed_host_gbs": round(moved / (ms_str * 1e-3) / 1e9, 2),
+            "streamed_equals_resident": same,
+            "note": "resident: norm-rope + MLP of every chunk with inputs and outputs in HBM; streamed: Q, K, x "
+                    "uploaded and Q', K', y downloaded through pinned host memory, double-buffered"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the W4A8 and long-sequence measurements")
     ap.add_argument("--cpu-sample-rows", type=int, default=2048)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (reference for HBM byte counters)")
@@ -204,6 +301,16 @@ def main() -> int:
     nr_gbs = nr_bytes / (nr_ms * 1e-3) / 1e9
     log(f"norm_rope: {nr_ms * 1e3:.1f} us/launch, {nr_gbs:.0f} GB/s ({nr_gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
+    # ------------------------------------------------------------------ W4A8 and long sequence
+    w4 = long = None
+    if not args.no_extra:
+        w4 = bench_w4a8(pkg, dev, max(3, args.steps // 4), 2)
+        log(f"w4a8 mlp: {w4['ms_per_step']:.3f} ms/step ({w4['value']} TOPS)")
+        long = bench_long(pkg, dev, inp, args.warmup)
+        log(f"long: resident {long['resident_ms']:.2f} ms ({long['resident_mlp_tops']} MLP TOPS), "
+            f"streamed {long['streamed_ms']:.2f} ms ({long['streamed_host_gbs']} GB/s of host I/O), "
+            f"equal={long['streamed_equals_resident']}")
+
     # ------------------------------------------------------------------ CPU baseline
     cpu = None
     cpu_nr = None
@@ -232,19 +339,21 @@ def main() -> int:
                    "norm_rope_workload": "norm_rope_720p", "grid": [7, 45, 80], "heads": 40, "head_dim": 128},
         "frac_of_peak": round(tops / PEAK_INT8_TOPS, 4),
         "kernels_ms": {k: round(v, 4) for k, v in kavg.items()},
-        "roofline": {"kernel": "gemm_i8_dma_kernel (fc1, dequant+GELU+row-amax epilogue)", "bound": "mfma",
+        "roofline": {"kernel": "gemm_i8_v5_kernel (fc1, dequant+GELU+row-amax epilogue)", "bound": "mfma",
                      "achieved": round(fc1_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(fc1_tops / PEAK_INT8_TOPS, 4),
                      "traffic": round(TRAFFIC_BYTES["fc1_gemm_gelu"]),
                      "algorithmic": "2*M*d*ffn int8 ops per launch (unit: 1e12 int8 ops/s)"},
-        "roofline_fc2": {"kernel": "gemm_i8_dma_kernel (fc2, dequant epilogue)", "bound": "mfma",
+        "roofline_fc2": {"kernel": "gemm_i8_v5_kernel (fc2, dequant epilogue)", "bound": "mfma",
                          "achieved": round(fc2_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                          "frac": round(fc2_tops / PEAK_INT8_TOPS, 4),
                          "traffic": round(TRAFFIC_BYTES["fc2_gemm"])},
-        "norm_rope": {"kernel": "rowspan_exact_kernel (Q and K)", "bound": "hbm", "achieved": round(nr_gbs, 1),
+        "norm_rope": {"kernel": "norm_rope_pipe_kernel (Q and K)", "bound": "hbm", "achieved": round(nr_gbs, 1),
                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(nr_gbs / PEAK_HBM_GBS, 4),
                       "us_per_launch": round(nr_ms * 1e3, 2), "traffic": round(TRAFFIC_BYTES["norm_rope"]),
                       "algorithmic": "8*M*d bytes (Q,K read + written, bf16)"},
+        "w4a8_mlp": w4,
+        "long": long,
         "cpu_baseline": cpu,
         "cpu_baseline_norm_rope": cpu_nr,
     }

@@ -449,3 +449,33 @@ def test_h3_segmented_rms_adaln(pkg, dev):
     want = cpu_ref.rms_adaln_segmented(x, w, sh, sc, segs, eps=1e-5)
     close(out, want, "segmented rms_adaln")
     assert same(out, want, "segmented rms_adaln")
+
+
+# --------------------------------------------------------------------------- token-chunked driver
+
+def test_long_driver_chunks_match_whole(pkg, dev):
+    """Chunking is exact (every op is per token): the chunked resident run and
+    the double-buffered host-streamed run both equal one whole-sequence call."""
+    say("long driver: 868 tokens in chunks of 256, resident and streamed")
+    from x_minimaxh3_amd import backend, driver, workloads
+
+    m, d, f, chunk = 868, 1024, 2048, 256
+    inp = workloads.mlp_inputs(M=m, d=d, ffn=f, n_outlier=4, seed=7)
+    g = torch.Generator().manual_seed(8)
+    q = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    scale = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
+    shift = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
+    freqs = workloads.rope_table_3d((2, 14, 31)).to(dev)
+    x, w1, s1, w2, s2 = (inp[n].to(dev) for n in ("x", "w1", "s1", "w2", "s2"))
+    qd, kd, scd, shd = q.to(dev), k.to(dev), scale.to(dev), shift.to(dev)
+    drv = driver.LongBlockDriver(w1, s1, w2, s2, scd, shd, chunk=chunk)
+    qo, ko, y = drv.run_resident(qd, kd, x, freqs)
+    wq, wk = backend.norm_rope(qd, kd, scd, shd, freqs)
+    wy = backend.w8a8_mlp(x, w1, s1, w2, s2)
+    torch.cuda.synchronize()
+    assert torch.equal(qo, wq) and torch.equal(ko, wk) and torch.equal(y, wy)
+    host = {n: torch.empty(m, d, dtype=torch.bfloat16, pin_memory=True) for n in ("qo", "ko", "y")}
+    drv.run_streamed(q.pin_memory(), k.pin_memory(), inp["x"].pin_memory(), freqs, host["qo"], host["ko"], host["y"])
+    assert torch.equal(host["qo"], wq.cpu()) and torch.equal(host["ko"], wk.cpu()) and torch.equal(host["y"], wy.cpu())
+    close(host["y"], cpu_ref.w8a8_mlp(inp["x"], inp["w1"], inp["s1"], inp["w2"], inp["s2"]), "streamed mlp vs oracle")

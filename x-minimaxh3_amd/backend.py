@@ -445,10 +445,12 @@ def rms_rope_split_half_(q, k, freqs_cis, q_scale, k_scale=None, epsilon=1e-6, r
 
 def norm_rope(q: torch.Tensor, k: torch.Tensor | None, scale: torch.Tensor, shift: torch.Tensor,
               freqs_cis: torch.Tensor, eps: float = 1e-6, head_dim: int = 128,
-              inplace: bool = False):
+              inplace: bool = False, out: tuple | None = None):
     """Fused rms_adaln (RMS over the full row) + split-half RoPE per head for
     Q and K of the same tokens. q/k: [..., tokens, width]; scale/shift rows
-    broadcast over tokens; freqs: [1, tokens or 1, 1, head_dim/2, 2, 2]."""
+    broadcast over tokens; freqs: [1, tokens or 1, 1, head_dim/2, 2, 2].
+    out: optional (q_out, k_out) with q's shape and dtype, rows 16-byte
+    aligned with a unit last stride (k_out None when k is None)."""
     width = q.shape[-1]
     if width % head_dim:
         raise ValueError(f"width {width} is not a multiple of head_dim {head_dim}")
@@ -474,8 +476,25 @@ def norm_rope(q: torch.Tensor, k: torch.Tensor | None, scale: torch.Tensor, shif
         raise ValueError(f"freqs_cis holds {ft.shape[0]} token rows for {m} tokens")
     ft = ft.contiguous()
     fstride = 0 if ft.shape[0] == 1 else ft.stride(0)
+    if inplace and out is not None:
+        raise ValueError("norm_rope: inplace and out are exclusive")
     if inplace:
         qo, ko = q2, k2
+    elif out is not None:
+        qo, ko = out
+        if (ko is None) != (k2 is None):
+            raise ValueError("norm_rope: out must hold a K output exactly when k is given")
+        for o in (qo, ko):
+            if o is None:
+                continue
+            if o.shape != q.shape or o.dtype != q.dtype or o.stride(-1) != 1:
+                raise ValueError("norm_rope: out tensors must have q's shape and dtype, unit last stride")
+        qo = qo.reshape(m, width)
+        ko = None if ko is None else ko.reshape(m, width)
+        if ko is not None and ko.stride(0) != qo.stride(0):
+            raise ValueError("norm_rope: q_out and k_out must have the same row stride")
+        if (qo.stride(0) * qo.element_size()) % 16 or qo.data_ptr() % 16 or (ko is not None and ko.data_ptr() % 16):
+            raise ValueError("norm_rope: out rows must be 16-byte aligned")
     else:
         qo = torch.empty(m, width, dtype=q.dtype, device=q.device)
         ko = None if k2 is None else torch.empty(m, width, dtype=q.dtype, device=q.device)
@@ -489,6 +508,8 @@ def norm_rope(q: torch.Tensor, k: torch.Tensor | None, scale: torch.Tensor, shif
         if k is not None and k2.data_ptr() != k.data_ptr():
             k.copy_(k2.reshape(k.shape))
         return q, k
+    if out is not None:
+        return out
     return qo.reshape(q.shape), (None if ko is None else ko.reshape(k.shape))
 
 
