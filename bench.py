@@ -45,9 +45,9 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 # 0.5 GiB by FETCH_SIZE and 1 GiB by WRITE_SIZE, so FETCH_SIZE is scaled x2 and
 # WRITE_SIZE x1 (see profiles/).
 TRAFFIC_BYTES = {
-    "fc1_gemm_gelu": (1432752.5 * 2 + 691031.8) * 1024,
-    "fc2_gemm": (1480923.4 * 2 + 252000.0) * 1024,
-    "norm_rope": (265271.7 * 2 + 504000.0) * 1024,
+    "fc1_gemm_gelu": (1499110.6 * 2 + 701725.0) * 1024,
+    "fc2_gemm": (1478203.0 * 2 + 255960.0) * 1024,
+    "norm_rope": (265143.7 * 2 + 504016.5) * 1024,
 }
 
 
@@ -61,6 +61,7 @@ def cpu_baseline_mlp(inp: dict, sample_rows: int, repeats: int = 3) -> dict:
     from oracle import cpu_ref
 
     torch.set_num_threads(os.cpu_count() or 1)
+    sample_rows = sample_rows or inp["x"].shape[0]
     x = inp["x"][:sample_rows]
     args = (inp["w1"], inp["s1"], inp["w2"], inp["s2"])
     cpu_ref.w8a8_mlp(x[:64], *args)          # warm-up
@@ -191,7 +192,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the W4A8 and long-sequence measurements")
-    ap.add_argument("--cpu-sample-rows", type=int, default=2048)
+    ap.add_argument("--cpu-sample-rows", type=int, default=0, help="tokens of the CPU baseline (0 = all)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (reference for HBM byte counters)")
     args = ap.parse_args()
