@@ -10,7 +10,7 @@
  *   - dtype codes follow the reference's op boundary
  *     (CK/backends/eager/quantization.py:34-42): 0 fp32, 1 fp16, 2 bf16.
  *   - input-activation codes follow CK/backends/_activations.py:19-24:
- *     0 none, 1 gelu_tanh (2 swiglu is not implemented here).
+ *     0 none, 1 gelu_tanh, 2 swiglu (swiglu only through the ConvRot quantizer).
  *   - Every entry point returns 0 on success, 1 invalid argument, 2 HIP
  *     launch error, 3 unsupported combination; the message is available from
  *     xmh3_last_error() on the calling thread. No C++ exception crosses the
@@ -55,6 +55,26 @@ int xmh3_quantize_int8_rowwise(const void* x, int x_dtype, int input_act, int64_
 int xmh3_quantize_int8_rowwise_ex(const void* x, int x_dtype, int input_act, int64_t M, int64_t K,
                                   int64_t ldx, int8_t* q, float* scale, uint32_t* clear_rows,
                                   xmh3_stream_t stream);
+
+/*
+ * Per-token int8 quantisation of a rotated linear's input:
+ *   a = act(x)  (input_act 0 none, 1 gelu_tanh, 2 swiglu: x rows are
+ *               [gate | up], 2*K wide, a = T(T(silu(gate)) * up))
+ *   r = T(a_g @ H) per group of 256 columns (H = H4 (x) H4 (x) H4 (x) H4 / 16)
+ *   (q, scale) = quantize_int8_rowwise(r)
+ * group_size 256 (the only ConvRot group the fused path takes) or 0 (no
+ * rotation; then input_act must be 2). K (the activated width) % 256 == 0,
+ * K <= 16384; x rows 16-byte aligned (ldx % 8 == 0); x bf16 or fp16.
+ * q: int8 [M, K] contiguous; scale: fp32 [M].
+ * Replaces: CK/backends/cuda/ops/int8_linear.cu:1295
+ *   launch_quantize_int8_rowwise_convrot64_kernel(input, output, scales, rows,
+ *   cols, group_size, dtype, stochastic, act_code, block_threads, seed, stream)
+ * (semantics of CK/backends/eager/quantization.py:998-1023 with convrot=True,
+ * CK/tensor/int8_utils.py:11-74, CK/backends/_activations.py:40-53).
+ */
+int xmh3_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int input_act, int64_t M, int64_t K,
+                                       int64_t ldx, int group_size, int8_t* q, float* scale,
+                                       xmh3_stream_t stream);
 
 /*
  * Requantise rows whose |max| is already known (bit pattern of the fp32

@@ -26,6 +26,12 @@ live in ``tests/test_oracle.py``):
 * ``quantize_w4_weight`` / ``dequant_int4_grouped_to_int8`` -- numpy
   restatement, pure-Python loops on tiny inputs, nibble-order and
   round-trip invariants.
+* ``build_hadamard`` / ``rotate_activation`` / ``rotate_weight`` -- the
+  closed form H[p][q] = prod_d H4[p_d][q_d] / 16 over base-4 digits,
+  symmetry and H @ H = I, one-hot columns, and float64 x @ H within one bf16
+  rounding; ``quantize_convrot`` is their composition with
+  ``quantize_int8_rowwise`` (parity unpinned at the last bit of the rotated
+  row: the reference's bf16 matmul accumulates in a library-defined order).
 * ``rms_adaln`` / ``rms_norm`` -- float64 closed form within 1 bf16 ulp and
   the special case scale=shift=0 reducing to ``F.rms_norm``.
 * ``rope_table``             -- closed form (cos/sin of integer position
@@ -128,14 +134,62 @@ def dequant(acc: torch.Tensor, x_scale: torch.Tensor, w_scale: torch.Tensor,
     return out
 
 
+# ---------------------------------------------------------------------------
+# ConvRot: the online Hadamard rotation of the rotated linears
+# ---------------------------------------------------------------------------
+
+def build_hadamard(size: int, dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """CK/tensor/int8_utils.py:11-39: the regular Hadamard matrix
+    H4 (x) H4 (x) ... (size a power of 4), normalised by 1/sqrt(size)."""
+    if size < 4 or (size & (size - 1)) != 0 or math.log(size, 4) % 1 != 0:
+        raise ValueError(f"Regular Hadamard size must be a power of 4, got {size}")
+    h4 = torch.tensor([[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]], dtype=dtype)
+    h = h4
+    n = 4
+    while n < size:
+        h = torch.kron(h, h4)
+        n *= 4
+    return h / (size ** 0.5)
+
+
+def rotate_activation(x: torch.Tensor, group_size: int) -> torch.Tensor:
+    """CK/tensor/int8_utils.py:58-74 as called by the eager int8_linear
+    (CK/backends/eager/quantization.py:1012-1017): per group of group_size
+    columns x_g @ H, H built in x's dtype, the matmul in x's dtype."""
+    k = x.shape[-1]
+    if k % group_size != 0:
+        raise ValueError(f"features {k} not divisible by group_size {group_size}")
+    h = build_hadamard(group_size).to(x.dtype)
+    return torch.matmul(x.reshape(-1, k // group_size, group_size), h).reshape(x.shape)
+
+
+def rotate_weight(w: torch.Tensor, group_size: int) -> torch.Tensor:
+    """CK/tensor/int8_utils.py:42-55: W_rot = W_g @ H^T offline (fp32)."""
+    n, k = w.shape
+    h = build_hadamard(group_size).to(w.dtype)
+    return torch.matmul(w.reshape(n, k // group_size, group_size), h.T).reshape(n, k)
+
+
+def quantize_convrot(x: torch.Tensor, group_size: int = 256, input_act: str | None = None):
+    """The quantizer of a rotated linear: act -> rotate -> quantize_int8_rowwise
+    (the eager order of CK/backends/eager/quantization.py:998-1023)."""
+    a = apply_input_act(x, input_act)
+    r = rotate_activation(a, group_size)
+    q, s = quantize_int8_rowwise(r.reshape(-1, r.shape[-1]))
+    return q, s, r
+
+
 def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
                 bias: torch.Tensor | None = None,
                 out_dtype: torch.dtype = torch.bfloat16,
                 input_act: str | None = None,
-                return_parts: bool = False):
-    """CK/backends/eager/quantization.py:971-1056 with convrot=False:
-    act -> rowwise quant -> int8 GEMM -> fp32 dequant -> cast -> bias."""
+                return_parts: bool = False,
+                convrot: bool = False, convrot_groupsize: int = 256):
+    """CK/backends/eager/quantization.py:971-1056:
+    act -> (rotate) -> rowwise quant -> int8 GEMM -> fp32 dequant -> cast -> bias."""
     x = apply_input_act(x, input_act)
+    if convrot:
+        x = rotate_activation(x, convrot_groupsize)
     if x.shape[-1] != weight.shape[-1]:
         raise ValueError("Input and weight inner dimensions must match")
     ws = weight_scale.to(torch.float32).reshape(-1)
@@ -218,12 +272,14 @@ def dequant_int4_grouped_to_int8(qdata: torch.Tensor, s_rel: torch.Tensor,
 def w4a8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor,
                 s_channel: torch.Tensor, group_size: int = 128,
                 bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
-                input_act: str | None = None) -> torch.Tensor:
-    """CK/backends/eager/w4a8_int8.py:457-508 without the forced ConvRot:
-    decode to the int8 grid, then int8_linear with s_channel as the
-    per-channel weight scale."""
+                input_act: str | None = None, convrot: bool = False,
+                convrot_groupsize: int = 256) -> torch.Tensor:
+    """CK/backends/eager/w4a8_int8.py:457-508: decode to the int8 grid, then
+    int8_linear with s_channel as the per-channel weight scale (the reference
+    always passes convrot=True; False gives the unrotated GELU-MLP form)."""
     w8 = dequant_int4_grouped_to_int8(qdata, s_rel, group_size)
-    return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype, input_act=input_act)
+    return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype, input_act=input_act,
+                       convrot=convrot, convrot_groupsize=convrot_groupsize)
 
 
 def w4a8_mlp(x, w1_packed, w1_srel, w1_sch, w2_packed, w2_srel, w2_sch, group_size=128):

@@ -42,10 +42,14 @@ def test_unimplemented_reference_features_raise(pkg):
 
     x = torch.randn(2, 256).bfloat16()
     w = torch.zeros(8, 256, dtype=torch.int8)
-    with pytest.raises(NotImplementedError, match="ConvRot"):
-        backend.int8_linear(x, w, torch.ones(8), convrot=True)
-    with pytest.raises(NotImplementedError, match="swiglu"):
-        backend.int8_linear(x, w, torch.ones(8), input_act="swiglu")
+    with pytest.raises(NotImplementedError, match="ConvRot group size 64"):
+        backend.int8_linear(x, w, torch.ones(8), convrot=True, convrot_groupsize=64)
+    with pytest.raises(NotImplementedError, match="activated width 128"):
+        backend.int8_linear(x, w[:, :128].contiguous(), torch.ones(8), input_act="swiglu")
+    with pytest.raises(NotImplementedError, match="dtype"):
+        backend.int8_linear(x.float(), w, torch.ones(8), convrot=True)
+    with pytest.raises(ValueError, match="inner dimensions"):
+        backend.int8_linear(torch.randn(2, 512).bfloat16(), w, torch.ones(8), input_act="gelu_tanh")
     with pytest.raises(ValueError, match="unsupported input_act"):
         backend.int8_linear(x, w, torch.ones(8), input_act="relu")
     with pytest.raises(ValueError, match="inner dimensions"):

@@ -479,3 +479,93 @@ def test_long_driver_chunks_match_whole(pkg, dev):
     drv.run_streamed(q.pin_memory(), k.pin_memory(), inp["x"].pin_memory(), freqs, host["qo"], host["ko"], host["y"])
     assert torch.equal(host["qo"], wq.cpu()) and torch.equal(host["ko"], wk.cpu()) and torch.equal(host["y"], wy.cpu())
     close(host["y"], cpu_ref.w8a8_mlp(inp["x"], inp["w1"], inp["s1"], inp["w2"], inp["s2"]), "streamed mlp vs oracle")
+
+
+# --------------------------------------------------------------------------- ConvRot / swiglu quantizer
+
+def _code_stats(q, qr, what):
+    q, qr = q.cpu(), qr
+    mism = (q != qr).float().mean().item()
+    dq = (q.int() - qr.int()).abs().max().item() if q.numel() else 0
+    say(f"  {what}: code mismatch rate {mism:.2e}, max code delta {dq}")
+    return mism, dq
+
+
+@pytest.mark.parametrize("m,k,act", [
+    (333, 1024, None),
+    (64, 5120, "gelu_tanh"),
+    (250, 13824, "swiglu"),       # raw rows 27648 wide: [gate | up]
+    (5, 256, "swiglu"),
+    (17, 16384, None),            # the widest activated row
+])
+def test_convrot_quantizer(pkg, dev, m, k, act):
+    say(f"convrot quantizer m={m} k={k} act={act}")
+    from x_minimaxh3_amd import backend
+
+    width = 2 * k if act == "swiglu" else k
+    x = outlier_acts(m, width, seed=m + k) * 0.5
+    q, s = backend.quantize_int8_rowwise_convrot64(x.to(dev), 256, input_act=act)
+    torch.cuda.synchronize()
+    qr, sr, r = cpu_ref.quantize_convrot(x, 256, act)
+    assert q.shape == qr.shape and s.shape == sr.shape
+    assert torch.allclose(s.cpu(), sr, rtol=2 ** -7, atol=0)
+    mism, dq = _code_stats(q, qr, "convrot codes")
+    assert mism < 2e-3 and dq <= 1
+    # for information: the reference's own quantization error in code steps
+    # (rint, the bf16 rounding of r / bf16(s), and bf16(s) against s)
+    err = (q.cpu().float() * s.cpu() - r.float()).abs() / s.cpu()
+    say(f"  max |q*s - r| / s = {err.max().item():.3f} (reference rule; codes compared above)")
+
+
+def test_swiglu_quantizer_without_rotation(pkg, dev):
+    say("swiglu quantizer, no rotation")
+    from x_minimaxh3_amd import backend
+
+    x = outlier_acts(100, 2 * 2048, seed=4)
+    q, s = backend._quantize(x.to(dev), 2)
+    torch.cuda.synchronize()
+    qr, sr = cpu_ref.quantize_int8_rowwise(cpu_ref.apply_input_act(x, "swiglu"))
+    assert torch.allclose(s.cpu(), sr, rtol=2 ** -7, atol=0)
+    mism, dq = _code_stats(q, qr, "swiglu codes")
+    assert mism < 2e-3 and dq <= 1
+
+
+def test_int8_linear_convrot_swiglu(pkg, dev):
+    """The H3 fc2 boundary: int8_linear(raw, W_rot, s, convrot=True,
+    convrot_groupsize=256, input_act="swiglu") on [gate | up] rows."""
+    say("int8_linear convrot + swiglu")
+    g = torch.Generator().manual_seed(31)
+    m, k, n = 300, 2048, 640
+    # gate/up of unit scale and fc2-like weights keep |y| near 1, where the
+    # 2e-2 bound sits above one bf16 step: the rotated row's last fp32 bit
+    # depends on the summation order, so a few codes may move by one
+    raw = torch.randn(m, 2 * k, generator=g).to(torch.bfloat16)
+    w = torch.randn(n, k, generator=g) * 0.01
+    w_rot = cpu_ref.rotate_weight(w, 256)
+    qw, sw = cpu_ref.quantize_int8_rowwise(w_rot)
+    y = pkg.int8_linear(raw.to(dev), qw.to(dev), sw.reshape(-1).to(dev), None, torch.bfloat16, convrot=True,
+                        convrot_groupsize=256, input_act="swiglu")
+    torch.cuda.synchronize()
+    yr = cpu_ref.int8_linear(raw, qw, sw.reshape(-1), input_act="swiglu", convrot=True, convrot_groupsize=256)
+    close(y, yr, "int8_linear convrot swiglu")
+    # rotation cancels: close to the unrotated float product
+    yf = (cpu_ref.apply_input_act(raw, "swiglu").float() @ w.T)
+    cs = cos_sim(y.cpu().float(), yf)
+    say(f"  cosine to the unrotated fp32 product: {cs:.5f}")
+    assert cs > 0.999
+
+
+def test_w4a8_linear_convrot(pkg, dev):
+    say("w4a8 linear with ConvRot (the reference's default)")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(32)
+    m, k, n = 129, 1536, 384
+    x = outlier_acts(m, k, seed=33)
+    w_rot = cpu_ref.rotate_weight(torch.randn(n, k, generator=g) * 0.02, 256)
+    packed, srel, sch = cpu_ref.quantize_w4_weight(w_rot, 128)
+    y = backend.w4a8_int8_linear(x.to(dev), packed.to(dev), srel.to(dev), sch.to(dev), group_size=128,
+                                 convrot_groupsize=256)
+    torch.cuda.synchronize()
+    yr = cpu_ref.w4a8_linear(x, packed, srel.float(), sch, 128, convrot=True, convrot_groupsize=256)
+    close(y, yr, "w4a8 linear convrot")

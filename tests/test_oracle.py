@@ -290,3 +290,61 @@ def test_rms_norm_reduction_order_is_pinned(d):
     rr = (np.float32(1) / np.sqrt(((emu / np.float32(d)).astype(np.float32) + np.float32(1e-6)).astype(np.float32)))
     out = torch.from_numpy((xf.numpy() * rr.astype(np.float32)[:, None]).astype(np.float32)).to(torch.bfloat16)
     assert torch.equal(out, F.rms_norm(xb, (d,), eps=1e-6))
+
+
+# --------------------------------------------------------------------------- ConvRot
+
+def test_hadamard_closed_form_and_involution():
+    """H[p][q] = prod over base-4 digits d of H4[p_d][q_d] / 16 (the regular
+    Hadamard matrix built by Kronecker powers), symmetric, H @ H = I."""
+    h4 = [[1, 1, 1, -1], [1, 1, -1, 1], [1, -1, 1, 1], [-1, 1, 1, 1]]
+    h = cpu_ref.build_hadamard(256).double()
+    want = torch.empty(256, 256, dtype=torch.float64)
+    for p in range(256):
+        for q in range(256):
+            v = 1
+            for d in range(4):
+                v *= h4[(p >> (2 * d)) & 3][(q >> (2 * d)) & 3]
+            want[p, q] = v / 16.0
+    assert torch.equal(h, want)
+    assert torch.equal(h, h.T)
+    assert torch.equal(h @ h, torch.eye(256, dtype=torch.float64))
+    # H4 has -1 exactly on its anti-diagonal (the identity the GPU stages use)
+    assert all((h4[i][j] == -1) == (i + j == 3) for i in range(4) for j in range(4))
+    for size in (4, 16, 64):
+        hs = cpu_ref.build_hadamard(size).double()
+        assert torch.allclose(hs @ hs, torch.eye(size, dtype=torch.float64), atol=1e-12)
+    with pytest.raises(ValueError):
+        cpu_ref.build_hadamard(128)
+
+
+def test_rotate_activation_against_float64():
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(37, 1024, generator=g) * 3).to(torch.bfloat16)
+    r = cpu_ref.rotate_activation(x, 256)
+    h = cpu_ref.build_hadamard(256).double()
+    exact = (x.double().reshape(37, 4, 256) @ h).reshape(37, 1024)
+    ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp(min=2.0 ** -100))) - 7)
+    assert ((r.double() - exact).abs() <= ulp).all()      # one bf16 rounding of the exact sum
+    # a one-hot input picks a row of H (orientation of x @ H)
+    e = torch.zeros(1, 256, dtype=torch.bfloat16)
+    e[0, 37] = 1
+    assert torch.equal(cpu_ref.rotate_activation(e, 256).double(), h[37].reshape(1, 256))
+    # rotating weights offline and activations online leaves x @ W^T unchanged
+    w = torch.randn(16, 256, generator=g, dtype=torch.float64)
+    xd = torch.randn(5, 256, generator=g, dtype=torch.float64)
+    rw = cpu_ref.rotate_weight(w, 256)
+    assert torch.allclose((xd @ h) @ rw.T, xd @ w.T, atol=1e-10)
+
+
+def test_quantize_convrot_swiglu_composition():
+    """swiglu halves the row: gate | up -> silu(gate) * up, rotated per 256
+    columns, quantized per token."""
+    g = torch.Generator().manual_seed(12)
+    raw = torch.randn(9, 1024, generator=g).to(torch.bfloat16)
+    q, s, r = cpu_ref.quantize_convrot(raw, 256, "swiglu")
+    assert q.shape == (9, 512) and s.shape == (9, 1) and r.shape == (9, 512)
+    act = torch.nn.functional.silu(raw[:, :512]) * raw[:, 512:]
+    assert torch.equal(act, cpu_ref.apply_input_act(raw, "swiglu"))
+    qq, ss = cpu_ref.quantize_int8_rowwise(cpu_ref.rotate_activation(act, 256))
+    assert torch.equal(q, qq) and torch.equal(s, ss)

@@ -61,6 +61,11 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0):
 
 
 def _quantize(x: torch.Tensor, act: int):
+    if act == 2:     # swiglu halves the row: the activation-aware quantizer, no rotation
+        why = _convrot_supported(x, act, 0)
+        if why is not None:
+            raise NotImplementedError(f"input_act='swiglu': {why}")
+        return _quantize_convrot(x, act, 0)
     x2, m, k, ld = _aligned_rows(x)
     q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
     s = torch.empty(*x.shape[:-1], 1, dtype=torch.float32, device=x.device)
@@ -72,16 +77,59 @@ def _quantize(x: torch.Tensor, act: int):
     return q, s
 
 
-_ACT = {None: 0, "none": 0, "gelu_tanh": 1}
+_ACT = {None: 0, "none": 0, "gelu_tanh": 1, "swiglu": 2}
 
 
 def _act_code(input_act):
-    if input_act == "swiglu":
-        raise NotImplementedError("input_act='swiglu' is not implemented by the mi355x backend")
     if input_act not in _ACT:
         known = ["gelu_tanh", "none", "swiglu"]
         raise ValueError(f"unsupported input_act: {input_act!r} (expected one of {known})")
     return _ACT[input_act]
+
+
+def _convrot_supported(x: torch.Tensor, act: int, group_size: int) -> str | None:
+    """Why the fused ConvRot / swiglu quantizer cannot take x, or None."""
+    width = 2 if act == 2 else 1
+    k = x.shape[-1]
+    if group_size not in (0, 256):
+        return f"ConvRot group size {group_size} (the mi355x quantizer rotates groups of 256)"
+    if k % width:
+        return f"swiglu needs an even row width, got {k}"
+    ka = k // width
+    if ka % 256 or ka > 16384:
+        return f"activated width {ka} (the mi355x ConvRot/swiglu quantizer needs a multiple of 256, <= 16384)"
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        return f"dtype {x.dtype} (the mi355x ConvRot/swiglu quantizer takes bf16 or fp16)"
+    return None
+
+
+def quantize_int8_rowwise_convrot64(x: torch.Tensor, group_size: int, stochastic_rounding: int | None = 0,
+                                    input_act: str | None = None):
+    """Fused act -> ConvRot -> per-token int8 (CK/backends/cuda/__init__.py:1410-1438;
+    semantics CK/backends/eager/quantization.py:998-1023 with convrot=True).
+    Returns (int8 [..., K'], fp32 [..., 1]) with K' = K (or K/2 for swiglu)."""
+    if stochastic_rounding is not None and stochastic_rounding > 0:
+        raise NotImplementedError("stochastic rounding is not implemented by the mi355x backend")
+    act = _act_code(input_act)
+    why = _convrot_supported(x, act, group_size)
+    if why is not None:
+        raise NotImplementedError(f"ConvRot quantizer: {why}")
+    return _quantize_convrot(x, act, group_size)
+
+
+def _quantize_convrot(x: torch.Tensor, act: int, group_size: int):
+    if not x.is_cuda:
+        raise ValueError("the mi355x quantizer needs a GPU tensor")
+    x2, m, k, ld = _aligned_rows(x)
+    ka = k // (2 if act == 2 else 1)
+    q = torch.empty(*x.shape[:-1], ka, dtype=torch.int8, device=x.device)
+    s = torch.empty(*x.shape[:-1], 1, dtype=torch.float32, device=x.device)
+    if m and ka:
+        call("xmh3_quantize_int8_rowwise_convrot", x2.data_ptr(), DTYPE_CODE[x.dtype], act, m, ka, ld,
+             group_size, q.data_ptr(), s.data_ptr(), stream_of(x))
+    elif m:
+        s.fill_(1e-30)
+    return q, s
 
 
 def _gemm(q: torch.Tensor, sx: torch.Tensor, weight: torch.Tensor, ws: torch.Tensor,
@@ -107,16 +155,21 @@ def _gemm(q: torch.Tensor, sx: torch.Tensor, weight: torch.Tensor, ws: torch.Ten
 def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
                 bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
                 convrot: bool = False, convrot_groupsize: int = 256, input_act: str | None = None):
-    """CK/backends/eager/quantization.py:971-1056 (convrot=False):
-    act -> per-row int8 quant -> MFMA int8 GEMM with the fp32 dequant epilogue."""
-    if convrot:
-        raise NotImplementedError("ConvRot online rotation is not implemented by the mi355x backend")
+    """CK/backends/eager/quantization.py:971-1056:
+    act -> (ConvRot) -> per-row int8 quant -> MFMA int8 GEMM with the fp32
+    dequant epilogue. With convrot=True the weight is the offline-rotated one
+    (W_g @ H^T, as the reference's rotated linears store it)."""
     act = _act_code(input_act)
+    if convrot:
+        why = _convrot_supported(x, act, convrot_groupsize)
+        if why is not None:
+            raise NotImplementedError(f"ConvRot online rotation: {why}")
     if out_dtype is None:
         out_dtype = torch.bfloat16
-    if x.shape[-1] != weight.shape[-1]:
+    k_act = x.shape[-1] // (2 if act == 2 else 1)
+    if k_act != weight.shape[-1]:
         raise ValueError(
-            f"Input and weight inner dimensions must match, got {x.shape[-1]} and {weight.shape[-1]}")
+            f"Input and weight inner dimensions must match, got {k_act} and {weight.shape[-1]}")
     weight = weight.to(device=x.device)
     ws = weight_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
     if ws.numel() not in (1, weight.shape[0]):
@@ -124,7 +177,10 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
             f"INT8 weight scale must be scalar or per-output-channel, got {tuple(weight_scale.shape)} "
             f"for weight shape {tuple(weight.shape)}")
     lead = x.shape[:-1]
-    q, sx = _quantize(x.reshape(-1, x.shape[-1]), act)
+    if convrot:
+        q, sx = _quantize_convrot(x.reshape(-1, x.shape[-1]), act, convrot_groupsize)
+    else:
+        q, sx = _quantize(x.reshape(-1, x.shape[-1]), act)
     out = _gemm(q, sx, weight, ws, bias, out_dtype)
     return out.reshape(*lead, weight.shape[0])
 
@@ -183,18 +239,22 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
                      bias: torch.Tensor | None = None, group_size: int = 16, convrot_groupsize: int = 256,
                      out_dtype: torch.dtype = torch.bfloat16, convrot: bool = True):
     """CK/backends/eager/w4a8_int8.py:457-508: decode the grouped int4 storage
-    to the int8 grid, then int8_linear with s_channel as the per-channel scale.
-    The reference always rotates (ConvRot); ``convrot=False`` selects the
-    unrotated form used by the GELU MLP workloads."""
+    to the int8 grid, then int8_linear with s_channel as the per-channel scale
+    and the reference's ConvRot rotation of the activations (the stored
+    weights are the rotated ones). ``convrot=False`` selects the unrotated
+    form used by the GELU MLP workloads."""
     validate_w4a8_operands(qdata, s_rel, s_channel, codebook, correction, group_size, convrot_groupsize)
     if x.shape[-1] != qdata.shape[-1] * 2:
         raise ValueError(f"Input K={x.shape[-1]} does not match qdata K={qdata.shape[-1] * 2}")
     if correction is not None:
         raise NotImplementedError("asymmetric W4A8 (correction) is not implemented by the mi355x backend")
     if convrot:
-        raise NotImplementedError("ConvRot online rotation is not implemented by the mi355x backend")
+        why = _convrot_supported(x, 0, convrot_groupsize)
+        if why is not None:
+            raise NotImplementedError(f"ConvRot online rotation: {why}")
     w8 = dequant_int4_grouped_to_int8(qdata, s_rel, codebook, group_size)
-    return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype)
+    return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype, convrot=convrot,
+                       convrot_groupsize=convrot_groupsize)
 
 
 # --------------------------------------------------------------------------- MLP blocks
