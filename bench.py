@@ -135,6 +135,25 @@ def bench_w4a8(pkg, dev, steps: int, warmup: int) -> dict:
             "note": "both int4 weights decoded to the int8 grid on the GPU inside every step"}
 
 
+def bench_convrot(pkg, dev, steps: int, warmup: int) -> dict:
+    """The H3 fc2 input quantizer: SwiGLU over [gate | up] rows, ConvRot-256,
+    per-token int8 codes, on the 720p token count with H3's ffn=14336."""
+    import torch
+
+    from x_minimaxh3_amd import backend
+
+    m, k = 25200, 14336
+    g = torch.Generator(device=dev).manual_seed(3)
+    raw = torch.randn(m, 2 * k, device=dev, generator=g).bfloat16()
+    ms = timed(lambda: backend.quantize_int8_rowwise_convrot64(raw, 256, input_act="swiglu"), steps, warmup)
+    nbytes = m * (5.0 * k + 4)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": "convrot_swiglu_quant_h3", "tokens": m, "ffn": k, "group_size": 256,
+            "kernel": "convrot_quant_rows_kernel", "bound": "hbm", "us_per_launch": round(ms * 1e3, 2),
+            "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "algorithmic": "(5*ffn + 4) bytes per token: [gate | up] bf16 read, int8 codes + fp32 scale written"}
+
+
 def bench_long(pkg, dev, inp: dict, warmup: int) -> dict:
     import torch
 
@@ -303,10 +322,12 @@ def main() -> int:
     log(f"norm_rope: {nr_ms * 1e3:.1f} us/launch, {nr_gbs:.0f} GB/s ({nr_gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
     # ------------------------------------------------------------------ W4A8 and long sequence
-    w4 = long = None
+    w4 = long = cr = None
     if not args.no_extra:
         w4 = bench_w4a8(pkg, dev, max(3, args.steps // 4), 2)
         log(f"w4a8 mlp: {w4['ms_per_step']:.3f} ms/step ({w4['value']} TOPS)")
+        cr = bench_convrot(pkg, dev, args.steps, args.warmup)
+        log(f"convrot swiglu quant: {cr['us_per_launch']:.1f} us/launch, {cr['achieved']:.0f} GB/s")
         long = bench_long(pkg, dev, inp, args.warmup)
         log(f"long: resident {long['resident_ms']:.2f} ms ({long['resident_mlp_tops']} MLP TOPS), "
             f"streamed {long['streamed_ms']:.2f} ms ({long['streamed_host_gbs']} GB/s of host I/O), "
@@ -354,6 +375,7 @@ def main() -> int:
                       "us_per_launch": round(nr_ms * 1e3, 2), "traffic": round(TRAFFIC_BYTES["norm_rope"]),
                       "algorithmic": "8*M*d bytes (Q,K read + written, bf16)"},
         "w4a8_mlp": w4,
+        "convrot_quant": cr,
         "long": long,
         "cpu_baseline": cpu,
         "cpu_baseline_norm_rope": cpu_nr,

@@ -19,31 +19,49 @@
 // accumulation order inside its bf16 matmul is a library detail, so the last
 // bit of r may differ (the parity bar for this op is the tolerance).
 //
-// Layout: one wave per row. 16 lanes per 256-column group, lane l holding the
-// 16 consecutive columns 16*(l%16) .. +15 of group 4*it + l/16 in iteration it
-// (digits 0 and 1 of the column inside the lane, digit 2 across the lanes of a
-// quad, digit 3 across the four quads of a 16-lane row). The rotated row stays
-// in registers (packed 16-bit) until its |max| is known. With group size 0
-// the same kernel quantizes the swiglu activation without a rotation.
+// Layout: one block per row, W waves (W * NIT * 4 >= K / 256). In iteration
+// it, wave w takes the four groups 4 * (it * W + w) .. +3, one per 16-lane
+// row of the wave; lane l of a row holds the 16 consecutive columns
+// 16 * l .. +15 of its group (digits 0 and 1 of the column inside the lane,
+// digit 2 in lane bits 0-1, digit 3 in lane bits 2-3). The cross-lane stages
+// use DPP (quad permutes and 16-lane row rotations) and leave each lane with
+// the outputs of the mirrored lane 15 - l, so lane l stores its codes at
+// 16 * (15 - l). The rotated row stays in registers (packed 16-bit) until the
+// block knows its |max|. With group size 0 the same kernel quantizes the
+// swiglu activation without a rotation.
 #include "common.hpp"
 
 #include <type_traits>
 
 namespace xmh3 {
 
-// the sum of the four values held by the lanes that differ in bits m1 and m2
-// (m1 | m2) of the lane index, and the value of the lane with both bits
-// flipped
-__device__ __forceinline__ void quad_terms(float a, int m1, int m2, float& sum, float& mirror) {
-  const float t = a + __shfl_xor(a, m1, 64);
-  sum = t + __shfl_xor(t, m2, 64);
-  mirror = __shfl_xor(a, m1 | m2, 64);
+// DPP controls (quad_perm and row_ror encodings of the gfx9 DPP word)
+constexpr int DPP_QUAD_XOR1 = 0xb1;   // quad_perm:[1,0,3,2]
+constexpr int DPP_QUAD_XOR2 = 0x4e;   // quad_perm:[2,3,0,1]
+constexpr int DPP_ROW_ROR4 = 0x124;   // row_ror:4
+constexpr int DPP_ROW_ROR8 = 0x128;   // row_ror:8
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+// radix-4 stage across the four lanes that differ in one base-4 digit of the
+// lane index (C1 pairs digit values d and d ^ 2, C2 pairs d and d +- 1).
+// With a_d at lane d, H4's row 3 - d is (sum - 2 a_d): lane d returns the
+// output of lane 3 - d.
+template <int C1, int C2>
+__device__ __forceinline__ float h4_lanes_mirrored(float a) {
+  const float t = a + dpp_f<C1>(a);
+  const float s = t + dpp_f<C2>(t);
+  return __builtin_fmaf(a, -2.0f, s);
 }
 
 // in-lane radix-4 stage over 4 values: b_j = (a0 + a1 + a2 + a3) - 2 a_(3-j)
 __device__ __forceinline__ void h4_inlane(float& a0, float& a1, float& a2, float& a3) {
   const float s = (a0 + a1) + (a2 + a3);
-  const float b0 = s - 2.0f * a3, b1 = s - 2.0f * a2, b2 = s - 2.0f * a1, b3 = s - 2.0f * a0;
+  const float b0 = __builtin_fmaf(a3, -2.0f, s), b1 = __builtin_fmaf(a2, -2.0f, s);
+  const float b2 = __builtin_fmaf(a1, -2.0f, s), b3 = __builtin_fmaf(a0, -2.0f, s);
   a0 = b0; a1 = b1; a2 = b2; a3 = b3;
 }
 
@@ -60,44 +78,53 @@ __device__ __forceinline__ float cr_act_swiglu(float g, float u) {
   return T::round(s * u);
 }
 
+typedef uint32_t cr_u32x4 __attribute__((ext_vector_type(4)));
+
 template <typename T, int ACT, bool ROT, int NIT>
-__global__ __launch_bounds__(256) void convrot_quant_rows_kernel(
-    const typename T::storage* __restrict__ x, int64_t ldx, int64_t M, int K,
-    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale) {
+__global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
+    const typename T::storage* __restrict__ x, int64_t ldx, int K, int8_t* __restrict__ q, int64_t ldq,
+    float* __restrict__ scale) {
   using S = typename T::storage;
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;
+  __shared__ float wave_amax[8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
+  const int64_t row = blockIdx.x;
   const S* xr = x + row * ldx;
   const int groups = K >> 8;
   const int g16 = lane & 15;
+  // loads of every iteration first: 2 (4 with the up half) x 16 bytes each
+  cr_u32x4 raw[NIT][2], up[NIT][2];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int group = (it * nwaves + wave) * 4 + (lane >> 4);
+    if (group < groups) {
+      const int c = group * 256 + g16 * 16;
+      raw[it][0] = __builtin_nontemporal_load(reinterpret_cast<const cr_u32x4*>(xr + c));
+      raw[it][1] = __builtin_nontemporal_load(reinterpret_cast<const cr_u32x4*>(xr + c + 8));
+      if constexpr (ACT == ACT_SWIGLU) {
+        up[it][0] = __builtin_nontemporal_load(reinterpret_cast<const cr_u32x4*>(xr + K + c));
+        up[it][1] = __builtin_nontemporal_load(reinterpret_cast<const cr_u32x4*>(xr + K + c + 8));
+      }
+    } else {
+      raw[it][0] = raw[it][1] = up[it][0] = up[it][1] = cr_u32x4{0u, 0u, 0u, 0u};
+    }
+  }
   uint32_t keep[NIT][8];                  // rotated values, T bits packed in pairs
   float amax = 0.0f;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
-    const int group = it * 4 + (lane >> 4);
-    const bool live = group < groups;
-    const int c = (live ? group : 0) * 256 + g16 * 16;
-    // 16 values = two 16-byte loads (and two more for the up half)
-    uint32_t raw[8], up[8];
-    {
-      const uint4 r0 = *reinterpret_cast<const uint4*>(xr + c), r1 = *reinterpret_cast<const uint4*>(xr + c + 8);
-      raw[0] = r0.x; raw[1] = r0.y; raw[2] = r0.z; raw[3] = r0.w;
-      raw[4] = r1.x; raw[5] = r1.y; raw[6] = r1.z; raw[7] = r1.w;
-      if constexpr (ACT == ACT_SWIGLU) {
-        const uint4 u0 = *reinterpret_cast<const uint4*>(xr + K + c);
-        const uint4 u1 = *reinterpret_cast<const uint4*>(xr + K + c + 8);
-        up[0] = u0.x; up[1] = u0.y; up[2] = u0.z; up[3] = u0.w;
-        up[4] = u1.x; up[5] = u1.y; up[6] = u1.z; up[7] = u1.w;
-      }
-    }
     float v[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float xi = T::load((raw[i >> 1] >> (16 * (i & 1))) & 0xffffu);
-      if constexpr (ACT == ACT_SWIGLU) v[i] = cr_act_swiglu<T>(xi, T::load((up[i >> 1] >> (16 * (i & 1))) & 0xffffu));
-      else if constexpr (ACT == ACT_GELU_TANH) v[i] = cr_act_gelu<T>(xi);
-      else v[i] = xi;
+      const uint32_t w = raw[it][i >> 3][(i >> 1) & 3];
+      const float xi = T::load((w >> (16 * (i & 1))) & 0xffffu);
+      if constexpr (ACT == ACT_SWIGLU) {
+        const uint32_t wu = up[it][i >> 3][(i >> 1) & 3];
+        v[i] = cr_act_swiglu<T>(xi, T::load((wu >> (16 * (i & 1))) & 0xffffu));
+      } else if constexpr (ACT == ACT_GELU_TANH) {
+        v[i] = cr_act_gelu<T>(xi);
+      } else {
+        v[i] = xi;
+      }
     }
     if constexpr (ROT) {
       // digit 0 (i & 3) and digit 1 (i >> 2), inside the lane
@@ -105,27 +132,30 @@ __global__ __launch_bounds__(256) void convrot_quant_rows_kernel(
       for (int d1 = 0; d1 < 4; ++d1) h4_inlane(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
 #pragma unroll
       for (int d0 = 0; d0 < 4; ++d0) h4_inlane(v[d0], v[4 + d0], v[8 + d0], v[12 + d0]);
-      // digit 2 (lane bits 0-1) and digit 3 (lane bits 2-3), across lanes
+      // digit 2 (lane bits 0-1), then digit 3 (lane bits 2-3), across lanes;
+      // H / 16 last (exact), before the rounding to the matmul's output dtype
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        float s, m;
-        quad_terms(v[i], 1, 2, s, m);
-        v[i] = s - 2.0f * m;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float s, m;
-        quad_terms(v[i], 4, 8, s, m);
-        v[i] = T::round((s - 2.0f * m) * 0.0625f);   // H / 16, then the matmul's output dtype
+        v[i] = h4_lanes_mirrored<DPP_QUAD_XOR1, DPP_QUAD_XOR2>(v[i]);
+        v[i] = h4_lanes_mirrored<DPP_ROW_ROR8, DPP_ROW_ROR4>(v[i]) * 0.0625f;
       }
     }
+    // |max| of the unrounded values: rounding is monotone, so T(max) is the
+    // max of the rounded row
+    const bool live = (it * nwaves + wave) * 4 + (lane >> 4) < groups;
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       if (live) amax = fmaxf(amax, fmaxf(fabsf(v[i]), fabsf(v[i + 1])));
-      keep[it][i >> 1] = (T::store(v[i]) & 0xffffu) | (T::store(v[i + 1]) << 16);
+      keep[it][i >> 1] = T::store2(v[i], v[i + 1]);
     }
   }
-  amax = wave_max(amax);
+  amax = T::round(wave_max(amax));
+  if (nwaves > 1) {
+    if (lane == 0) wave_amax[wave] = amax;
+    __syncthreads();
+    amax = wave_amax[0];
+    for (int w = 1; w < nwaves; ++w) amax = fmaxf(amax, wave_amax[w]);
+  }
   const float s = fmaxf(amax / 127.0f, 1e-30f);
   float sT = T::round(s);
   if (sT == 0.0f) sT = T::tiny();
@@ -133,7 +163,7 @@ __global__ __launch_bounds__(256) void convrot_quant_rows_kernel(
   int8_t* qr = q + row * ldq;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
-    const int group = it * 4 + (lane >> 4);
+    const int group = (it * nwaves + wave) * 4 + (lane >> 4);
     if (group >= groups) continue;
     uint32_t w[4];
 #pragma unroll
@@ -152,26 +182,29 @@ __global__ __launch_bounds__(256) void convrot_quant_rows_kernel(
       }
       w[k] = word;
     }
-    *reinterpret_cast<uint4*>(qr + group * 256 + g16 * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    const int slot = ROT ? 15 - g16 : g16;
+    *reinterpret_cast<uint4*>(qr + group * 256 + slot * 16) = make_uint4(w[0], w[1], w[2], w[3]);
   }
-  if (lane == 0) scale[row] = s;
+  if (threadIdx.x == 0) scale[row] = s;
 }
 
 template <typename T, int ACT, bool ROT>
 static int launch_convrot_T(const void* x, int64_t ldx, int64_t M, int K, int8_t* q, int64_t ldq, float* scale,
                             hipStream_t st) {
   using S = typename T::storage;
-  const int nit = (K / 256 + 3) / 4;
-  dim3 grid((unsigned)((M + 3) / 4));
-#define XMH3_CR(N)                                                                                   \
-  if (nit <= N) {                                                                                    \
-    hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, ROT, N>), grid, dim3(256), 0, st,          \
-                       static_cast<const S*>(x), ldx, M, K, q, ldq, scale);                          \
-    return check_launch("convrot_quant_rows_kernel");                                                \
-  }
-  XMH3_CR(1) XMH3_CR(2) XMH3_CR(4) XMH3_CR(8) XMH3_CR(12) XMH3_CR(16)
-#undef XMH3_CR
-  return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: activated row wider than 16384");
+  // wave-iterations of four groups each; at most 16 (K <= 16384)
+  const int quads = (K / 256 + 3) / 4;
+  const int nit = (quads + 7) / 8;
+  const int waves = (quads + nit - 1) / nit;
+  if (M > 0x7fffffff) return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: more than 2^31-1 rows");
+  const dim3 grid((unsigned)M), block((unsigned)(64 * waves));
+  if (nit == 1)
+    hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, ROT, 1>), grid, block, 0, st, static_cast<const S*>(x),
+                       ldx, K, q, ldq, scale);
+  else
+    hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, ROT, 2>), grid, block, 0, st, static_cast<const S*>(x),
+                       ldx, K, q, ldq, scale);
+  return check_launch("convrot_quant_rows_kernel");
 }
 
 int quantize_rows_convrot(const void* x, int x_dtype, int input_act, int64_t M, int64_t K, int64_t ldx,
