@@ -517,6 +517,50 @@ def test_convrot_quantizer(pkg, dev, m, k, act):
     say(f"  max |q*s - r| / s = {err.max().item():.3f} (reference rule; codes compared above)")
 
 
+def test_convrot_quantizer_exact_rows(pkg, dev):
+    """Rows whose rotation is exact in fp32 in any summation order
+    (small integers: every partial sum is an integer below 2^24) must give
+    the oracle's codes and scales bit for bit; a zero row gives zero codes and
+    the 1e-30 scale floor; a strided view reads the same rows."""
+    say("convrot quantizer on exact rows, zero rows, strided rows")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(77)
+    m, k = 67, 4096
+    x = torch.randint(-40, 41, (m, k), generator=g).float()
+    x[5] = 0.0
+    x[9, :] = 0.0
+    x[9, 300] = -1000.0      # a single spike spreads over its group
+    x = x.to(torch.bfloat16)
+    q, s = backend.quantize_int8_rowwise_convrot64(x.to(dev), 256)
+    torch.cuda.synchronize()
+    qr, sr, _ = cpu_ref.quantize_convrot(x, 256, None)
+    assert same(q, qr, "exact-row codes") and same(s, sr, "exact-row scales")
+    assert (q[5] == 0).all() and s[5].item() == pytest.approx(1e-30, rel=1e-6)
+    # the same rows inside a wider buffer (ldx = k + 512)
+    wide = torch.zeros(m, k + 512, dtype=torch.bfloat16)
+    wide[:, :k] = x
+    qv, sv = backend.quantize_int8_rowwise_convrot64(wide.to(dev)[:, :k], 256)
+    torch.cuda.synchronize()
+    assert same(qv, qr, "strided codes") and same(sv, sr, "strided scales")
+
+
+@pytest.mark.parametrize("act", [None, "gelu_tanh", "swiglu"])
+def test_convrot_quantizer_fp16(pkg, dev, act):
+    say(f"convrot quantizer, fp16 rows, act={act}")
+    from x_minimaxh3_amd import backend
+
+    m, k = 150, 3072
+    width = 2 * k if act == "swiglu" else k
+    x = (outlier_acts(m, width, seed=5) * 0.5).to(torch.float16)
+    q, s = backend.quantize_int8_rowwise_convrot64(x.to(dev), 256, input_act=act)
+    torch.cuda.synchronize()
+    qr, sr, _ = cpu_ref.quantize_convrot(x, 256, act)
+    assert torch.allclose(s.cpu(), sr, rtol=2 ** -10, atol=0)
+    mism, dq = _code_stats(q, qr, "fp16 convrot codes")
+    assert mism < 2e-3 and dq <= 1
+
+
 def test_swiglu_quantizer_without_rotation(pkg, dev):
     say("swiglu quantizer, no rotation")
     from x_minimaxh3_amd import backend

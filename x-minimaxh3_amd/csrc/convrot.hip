@@ -15,9 +15,12 @@
 // The rotation is evaluated in fp32 as four radix-4 stages (one per base-4
 // digit of the column inside its group; H4 is symmetric and
 // H4[i][j] = -1 exactly when i + j == 3, so a stage output is
-// sum(a_0..a_3) - 2 * a_(3-j)), then rounded to T once: the reference's fp32
-// accumulation order inside its bf16 matmul is a library detail, so the last
-// bit of r may differ (the parity bar for this op is the tolerance).
+// sum(a_0..a_3) - 2 * a_(3-j)), then rounded to T once. The reference's fp32
+// accumulation order inside its bf16 matmul is a library detail; every order
+// gives the same fp32 sums when they are exact (a group whose values span at
+// most about 8 binades), otherwise the last bit of r may differ. The stages
+// sum without the 1/16 (up to 256 |a|), so activations beyond 2^120 in
+// magnitude overflow here where the normalised matmul would still be finite.
 //
 // Layout: one block per row, W waves (W * NIT * 4 >= K / 256). In iteration
 // it, wave w takes the four groups 4 * (it * W + w) .. +3, one per 16-lane
@@ -26,8 +29,8 @@
 // digit 2 in lane bits 0-1, digit 3 in lane bits 2-3). The cross-lane stages
 // use DPP (quad permutes and 16-lane row rotations) and leave each lane with
 // the outputs of the mirrored lane 15 - l, so lane l stores its codes at
-// 16 * (15 - l). The rotated row stays in registers (packed 16-bit) until the
-// block knows its |max|. With group size 0 the same kernel quantizes the
+// 16 * (15 - l). The rotated row stays in registers (fp32 for bf16, packed
+// 16-bit for fp16) until the block knows its |max|. With group size 0 the same kernel quantizes the
 // swiglu activation without a rotation.
 #include "common.hpp"
 
@@ -108,7 +111,13 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
       raw[it][0] = raw[it][1] = up[it][0] = up[it][1] = cr_u32x4{0u, 0u, 0u, 0u};
     }
   }
-  uint32_t keep[NIT][8];                  // rotated values, T bits packed in pairs
+  // bf16: the rotated values stay in fp32 without the final 1/16 (T(16 r) is
+  // 16 T(r) exactly, and every code and the scale are taken from products
+  // with exact powers of two; a subnormal r has code 0 either way). fp16's
+  // narrower exponent range does not allow that: it keeps T(r) packed.
+  constexpr bool FOLD = std::is_same<T, BF16T>::value;
+  float keepf[FOLD ? NIT : 1][16];
+  uint32_t keep[FOLD ? 1 : NIT][8];
   float amax = 0.0f;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
@@ -132,21 +141,25 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
       for (int d1 = 0; d1 < 4; ++d1) h4_inlane(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
 #pragma unroll
       for (int d0 = 0; d0 < 4; ++d0) h4_inlane(v[d0], v[4 + d0], v[8 + d0], v[12 + d0]);
-      // digit 2 (lane bits 0-1), then digit 3 (lane bits 2-3), across lanes;
-      // H / 16 last (exact), before the rounding to the matmul's output dtype
+      // digit 2 (lane bits 0-1), then digit 3 (lane bits 2-3), across lanes
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         v[i] = h4_lanes_mirrored<DPP_QUAD_XOR1, DPP_QUAD_XOR2>(v[i]);
-        v[i] = h4_lanes_mirrored<DPP_ROW_ROR8, DPP_ROW_ROR4>(v[i]) * 0.0625f;
+        v[i] = h4_lanes_mirrored<DPP_ROW_ROR8, DPP_ROW_ROR4>(v[i]);
+        if constexpr (!FOLD) v[i] *= 0.0625f;   // H / 16 (exact)
       }
     }
-    // |max| of the unrounded values: rounding is monotone, so T(max) is the
-    // max of the rounded row
-    const bool live = (it * nwaves + wave) * 4 + (lane >> 4) < groups;
+    // |max| of the unrounded values (lanes past the last group hold zeros):
+    // rounding is monotone, so T(max) is the max of the rounded row
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      if (live) amax = fmaxf(amax, fmaxf(fabsf(v[i]), fabsf(v[i + 1])));
-      keep[it][i >> 1] = T::store2(v[i], v[i + 1]);
+      amax = fmaxf(amax, fmaxf(fabsf(v[i]), fabsf(v[i + 1])));
+      if constexpr (FOLD) {
+        keepf[it][i] = v[i];
+        keepf[it][i + 1] = v[i + 1];
+      } else {
+        keep[it][i >> 1] = T::store2(v[i], v[i + 1]);
+      }
     }
   }
   amax = T::round(wave_max(amax));
@@ -156,10 +169,12 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
     amax = wave_amax[0];
     for (int w = 1; w < nwaves; ++w) amax = fmaxf(amax, wave_amax[w]);
   }
-  const float s = fmaxf(amax / 127.0f, 1e-30f);
+  constexpr float unfold = (FOLD && ROT) ? 0.0625f : 1.0f;
+  const float s = fmaxf(amax * unfold / 127.0f, 1e-30f);
   float sT = T::round(s);
   if (sT == 0.0f) sT = T::tiny();
   const float inv = 1.0f / sT;
+  const float inv_v = inv * unfold;       // applied to the kept values
   int8_t* qr = q + row * ldq;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
@@ -168,19 +183,30 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
     uint32_t w[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      uint32_t word = 0;
+      if constexpr (FOLD) {
+        // rint(T(T(v) * inv)) clamped, as the low byte of c + 1.5 * 2^23 (the
+        // fp32 add rounds to the nearest even integer); four bytes by v_perm
+        uint32_t y[4];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int i = 4 * k + b;
-        const uint32_t bits = (keep[it][i >> 1] >> (16 * (i & 1))) & 0xffffu;
-        const float r = T::load(bits);
-        float code;
-        if constexpr (std::is_same<T, BF16T>::value) code = rintf(T::round(r * inv));   // see quant.hip
-        else code = rintf(T::round(r / sT));
-        code = fminf(fmaxf(code, -128.0f), 127.0f);
-        word |= (uint32_t)((int)code & 0xff) << (8 * b);
+        for (int b = 0; b < 4; ++b) {
+          const float c = T::round(T::round(keepf[it][4 * k + b]) * inv_v);
+          y[b] = __float_as_uint(__builtin_amdgcn_fmed3f(c, -128.0f, 127.0f) + 12582912.0f);
+        }
+        const uint32_t lo = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(y[3], y[2], 0x0c0c0400u);
+        w[k] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+      } else {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int i = 4 * k + b;
+          const float r = T::load((keep[it][i >> 1] >> (16 * (i & 1))) & 0xffffu);
+          float code = rintf(T::round(r / sT));
+          code = fminf(fmaxf(code, -128.0f), 127.0f);
+          word |= (uint32_t)((int)code & 0xff) << (8 * b);
+        }
+        w[k] = word;
       }
-      w[k] = word;
     }
     const int slot = ROT ? 15 - g16 : g16;
     *reinterpret_cast<uint4*>(qr + group * 256 + slot * 16) = make_uint4(w[0], w[1], w[2], w[3]);
