@@ -29,9 +29,11 @@ live in ``tests/test_oracle.py``):
 * ``build_hadamard`` / ``rotate_activation`` / ``rotate_weight`` -- the
   closed form H[p][q] = prod_d H4[p_d][q_d] / 16 over base-4 digits,
   symmetry and H @ H = I, one-hot columns, and float64 x @ H within one bf16
-  rounding; ``quantize_convrot`` is their composition with
-  ``quantize_int8_rowwise`` (parity unpinned at the last bit of the rotated
-  row: the reference's bf16 matmul accumulates in a library-defined order).
+  rounding, bit-exact on integer-valued rows (exact fp32 sums);
+  ``quantize_convrot`` is their composition with ``quantize_int8_rowwise``
+  (parity unpinned at the last bit of the rotated row where its fp32 sums are
+  inexact: the reference's bf16 matmul accumulates in a library-defined
+  order).
 * ``rms_adaln`` / ``rms_norm`` -- float64 closed form within 1 bf16 ulp and
   the special case scale=shift=0 reducing to ``F.rms_norm``.
 * ``rope_table``             -- closed form (cos/sin of integer position

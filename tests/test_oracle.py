@@ -326,6 +326,12 @@ def test_rotate_activation_against_float64():
     exact = (x.double().reshape(37, 4, 256) @ h).reshape(37, 1024)
     ulp = torch.pow(2.0, torch.floor(torch.log2(exact.abs().clamp(min=2.0 ** -100))) - 7)
     assert ((r.double() - exact).abs() <= ulp).all()      # one bf16 rounding of the exact sum
+    # integer-valued rows: every fp32 partial sum is exact, so the rotation is
+    # the exact product rounded once to bf16, bit for bit
+    xi = torch.randint(-40, 41, (23, 1024), generator=g).to(torch.bfloat16)
+    ri = cpu_ref.rotate_activation(xi, 256)
+    exact_i = (xi.double().reshape(23, 4, 256) @ h).reshape(23, 1024)
+    assert torch.equal(ri, exact_i.to(torch.bfloat16))
     # a one-hot input picks a row of H (orientation of x @ H)
     e = torch.zeros(1, 256, dtype=torch.bfloat16)
     e[0, 37] = 1
