@@ -106,6 +106,26 @@ int xmh3_int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, i
                    uint32_t* row_absmax_bits, xmh3_stream_t stream);
 
 /*
+ * fc2 of the H3 block with its gated residual update, in place:
+ *   y = T(float(acc) * (sx[m] * sw[n])) (+ bias[n] in T)
+ *   residual[m, n] = T(residual[m, n] + y * T(gate[gate_rows[m], n]))
+ * T = the residual's dtype (bf16 or fp16); gate fp32 or T, [rows, ldg];
+ * gate_rows int32 [M] (the modulation segment row of each token, clamped into
+ * [0, gate_nrows) so a bad index cannot read past the table).
+ * N, ldr and ldg multiples of 4; residual 8-byte aligned (fp32 gate: 16).
+ * Replaces: h3serve/native_engine/model/fused_mlp.py:157-222
+ *   _fused_down_gated_residual(hidden, residual, gate, gate_rows, qweight,
+ *   weight_scale, bias) with its Triton kernel (fused_mlp.py:58-145), and the
+ *   default route it stands for, int8_linear then addcmul_ per segment
+ *   (fused_mlp.py:396-426, layers.py:937-953).
+ */
+int xmh3_int8_gemm_gated_residual(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_t M,
+                                  int64_t N, int64_t K, const float* sx, const float* sw, int sw_per_channel,
+                                  const void* bias, void* residual, int res_dtype, int64_t ldr,
+                                  const void* gate, int gate_dtype, int64_t ldg, int64_t gate_nrows,
+                                  const int32_t* gate_rows, xmh3_stream_t stream);
+
+/*
  * Grouped int4 -> int8 grid decode (low nibble = even k).
  * Replaces: CK/backends/cuda/ops/w4a8_gemm.cu:94
  *   launch_dequant_int4_grouped_to_int8(qw, s_rel, codebook, out, N, K, G, stream)

@@ -34,6 +34,11 @@ live in ``tests/test_oracle.py``):
   (parity unpinned at the last bit of the rotated row where its fp32 sums are
   inexact: the reference's bf16 matmul accumulates in a library-defined
   order).
+* ``segment_row_map`` / ``gated_residual_`` / ``int8_linear_gated_residual_``
+  -- the same torch ``addcmul_`` the reference calls; pinned by the float64
+  closed form (the product of two bf16 values is exact in fp32, so the result
+  is the exact r + y*g rounded once to fp32 and once to bf16) and by the
+  row-map equivalence with a per-token gather.
 * ``rms_adaln`` / ``rms_norm`` -- float64 closed form within 1 bf16 ulp and
   the special case scale=shift=0 reducing to ``F.rms_norm``.
 * ``rope_table``             -- closed form (cos/sin of integer position
@@ -205,6 +210,52 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
     if return_parts:
         return out, {"act": x2, "q": q, "scale": s, "acc": acc}
     return out
+
+
+# ---------------------------------------------------------------------------
+# the H3 fc2 boundary: projection, then the AdaLN-gated residual update
+# ---------------------------------------------------------------------------
+
+def segment_row_map(length: int, segments) -> torch.Tensor:
+    """int32 [length]: the modulation row of every token
+    (h3serve/native_engine/model/fused_mlp.py:34-55; the segments must be an
+    ordered partition of [0, length))."""
+    out = torch.empty(length, dtype=torch.int32)
+    previous = 0
+    for start, stop, row in segments:
+        if start != previous or stop <= start:
+            raise ValueError("modulation segments must be an ordered partition")
+        out[start:stop] = row
+        previous = stop
+    if previous != length:
+        raise ValueError("modulation segments do not cover the packed sequence")
+    return out
+
+
+def gated_residual_(residual: torch.Tensor, update: torch.Tensor, gate: torch.Tensor, segments) -> torch.Tensor:
+    """residual[a:b].addcmul_(update[a:b], gate[row].to(update.dtype)) per
+    segment (h3serve/native_engine/model/layers.py:937-953), in place."""
+    previous = 0
+    for start, stop, row in segments:
+        if start != previous or stop <= start:
+            raise ValueError("modulation segments must be an ordered partition")
+        residual[start:stop].addcmul_(update[start:stop], gate[row].to(update.dtype))
+        previous = stop
+    if previous != residual.shape[0]:
+        raise ValueError("modulation segments do not cover the packed sequence")
+    return residual
+
+
+def int8_linear_gated_residual_(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                                bias: torch.Tensor | None, residual: torch.Tensor, gate: torch.Tensor,
+                                segments, convrot: bool = True, convrot_groupsize: int = 256,
+                                input_act: str | None = "swiglu") -> torch.Tensor:
+    """The default fc2 route of the H3 block
+    (h3serve/native_engine/model/fused_mlp.py:396-426): int8_linear in the
+    residual's dtype, then the gated residual update per segment."""
+    projected = int8_linear(x, weight, weight_scale, bias, out_dtype=residual.dtype, input_act=input_act,
+                            convrot=convrot, convrot_groupsize=convrot_groupsize)
+    return gated_residual_(residual, projected, gate, segments)
 
 
 # ---------------------------------------------------------------------------

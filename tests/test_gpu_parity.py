@@ -613,3 +613,79 @@ def test_w4a8_linear_convrot(pkg, dev):
     torch.cuda.synchronize()
     yr = cpu_ref.w4a8_linear(x, packed, srel.float(), sch, 128, convrot=True, convrot_groupsize=256)
     close(y, yr, "w4a8 linear convrot")
+
+
+@pytest.mark.parametrize("m,n,k,dt,gate_dt,bias", [
+    (300, 640, 2048, torch.bfloat16, torch.float32, False),    # K % 256 == 0: the DMA main loop
+    (77, 260, 1040, torch.bfloat16, torch.bfloat16, True),     # K % 128 != 0: register-staged loop
+    (513, 384, 1536, torch.float16, torch.float16, True),
+])
+def test_int8_gemm_gated_residual(pkg, dev, m, n, k, dt, gate_dt, bias):
+    """fc2 with the gated residual in its epilogue against int8_linear then
+    addcmul_ per segment (no rotation and no act here, so every code and
+    accumulator is exact and the result must be bit-exact)."""
+    say(f"gated residual epilogue m={m} n={n} k={k} {dt} gate {gate_dt} bias={bias}")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(m + n)
+    x = outlier_acts(m, k, seed=m).to(dt)
+    w, sw = cpu_ref.quantize_int8_rowwise(torch.randn(n, k, generator=g) * 0.02)
+    b = (torch.randn(n, generator=g) * 0.1).to(dt) if bias else None
+    res = torch.randn(m, n, generator=g).to(dt)
+    gate = (torch.randn(4, n, generator=g) * 0.3).to(gate_dt)
+    cut = m // 3
+    segments = ((0, cut, 2), (cut, m, 1))
+    rows = cpu_ref.segment_row_map(m, segments)
+    want = cpu_ref.int8_linear_gated_residual_(x, w, sw.reshape(-1), b, res.clone(), gate, segments,
+                                               convrot=False, input_act=None)
+    got = res.to(dev)
+    backend.int8_linear_gated_residual_(x.to(dev), w.to(dev), sw.reshape(-1).to(dev),
+                                        None if b is None else b.to(dev), got, gate.to(dev), rows.to(dev),
+                                        convrot=False, input_act=None)
+    torch.cuda.synchronize()
+    assert same(got, want, "gated residual")
+
+
+def test_int8_gemm_gated_residual_clamps_rows(pkg, dev):
+    """A gate row index past the table reads its last row (no read past it)."""
+    say("gated residual: out-of-range gate rows are clamped")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(3)
+    m, n, k = 64, 256, 512
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    w, sw = cpu_ref.quantize_int8_rowwise(torch.randn(n, k, generator=g) * 0.02)
+    res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    gate = torch.randn(2, n, generator=g)
+    rows_bad = torch.full((m,), 7, dtype=torch.int32)
+    want = cpu_ref.int8_linear_gated_residual_(x, w, sw.reshape(-1), None, res.clone(), gate, ((0, m, 1),),
+                                               convrot=False, input_act=None)
+    got = res.to(dev)
+    backend.int8_linear_gated_residual_(x.to(dev), w.to(dev), sw.reshape(-1).to(dev), None, got, gate.to(dev),
+                                        rows_bad.to(dev), convrot=False, input_act=None)
+    torch.cuda.synchronize()
+    assert same(got, want, "clamped gate rows")
+
+
+def test_h3_gated_swiglu_mlp(pkg, dev):
+    """The int8 route of the H3 MLP (fc1 ConvRot linear -> SwiGLU + ConvRot
+    quantizer -> fc2 with the gated residual), chunked, against the oracle's
+    default route (int8_linear twice, then addcmul_ per segment)."""
+    say("H3 gated SwiGLU MLP, chunked")
+    from x_minimaxh3_amd import h3
+
+    g = torch.Generator().manual_seed(41)
+    m, d, f = 300, 512, 1024
+    hidden = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    w1, s1 = cpu_ref.quantize_int8_rowwise(cpu_ref.rotate_weight(torch.randn(2 * f, d, generator=g) * 0.05, 256))
+    w2, s2 = cpu_ref.quantize_int8_rowwise(cpu_ref.rotate_weight(torch.randn(d, f, generator=g) * 0.03, 256))
+    res = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    gate = torch.randn(2, d, generator=g) * 0.5
+    segments = ((0, 120, 1), (120, m, 0))
+    raw = cpu_ref.int8_linear(hidden, w1, s1.reshape(-1), None, torch.bfloat16, convrot=True)
+    want = cpu_ref.int8_linear_gated_residual_(raw, w2, s2.reshape(-1), None, res.clone(), gate, segments)
+    got = res.to(dev)
+    h3.gated_swiglu_mlp_(got, hidden.to(dev), w1.to(dev), s1.reshape(-1).to(dev), None, w2.to(dev),
+                         s2.reshape(-1).to(dev), None, gate.to(dev), segments, chunk_tokens=128)
+    torch.cuda.synchronize()
+    close(got, want, "h3 gated swiglu mlp")

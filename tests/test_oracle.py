@@ -354,3 +354,26 @@ def test_quantize_convrot_swiglu_composition():
     assert torch.equal(act, cpu_ref.apply_input_act(raw, "swiglu"))
     qq, ss = cpu_ref.quantize_int8_rowwise(cpu_ref.rotate_activation(act, 256))
     assert torch.equal(q, qq) and torch.equal(s, ss)
+
+
+def test_gated_residual_closed_form_and_row_map():
+    """residual.addcmul_(y, T(gate[row])) per segment: the product of two bf16
+    values is exact in fp32, so each output is r + y*g rounded once to fp32,
+    then to bf16; the segment form equals a per-token gather through the row
+    map."""
+    g = torch.Generator().manual_seed(21)
+    m, n = 97, 320
+    segments = ((0, 40, 2), (40, 41, 0), (41, 97, 1))
+    res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    upd = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    gate = torch.randn(3, n, generator=g) * 0.3          # fp32, as the modulation chunk
+    out = cpu_ref.gated_residual_(res.clone(), upd, gate, segments)
+    rows = cpu_ref.segment_row_map(m, segments)
+    assert rows.dtype == torch.int32 and rows[39] == 2 and rows[40] == 0 and rows[41] == 1
+    gt = gate.to(torch.bfloat16)[rows.long()].double()
+    exact = (res.double() + upd.double() * gt).float().to(torch.bfloat16)
+    assert torch.equal(out, exact)
+    with pytest.raises(ValueError):
+        cpu_ref.segment_row_map(m, ((0, 40, 0), (41, 97, 1)))
+    with pytest.raises(ValueError):
+        cpu_ref.gated_residual_(res.clone(), upd, gate, ((0, 50, 0),))

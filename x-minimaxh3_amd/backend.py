@@ -185,6 +185,77 @@ def int8_linear(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tenso
     return out.reshape(*lead, weight.shape[0])
 
 
+def int8_linear_gated_residual_(x: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor,
+                                bias: torch.Tensor | None, residual: torch.Tensor, gate: torch.Tensor,
+                                gate_rows: torch.Tensor, convrot: bool = True, convrot_groupsize: int = 256,
+                                input_act: str | None = "swiglu") -> torch.Tensor:
+    """residual[m] += int8_linear(x, weight, ...)[m] * gate[gate_rows[m]], in place.
+
+    The fc2 boundary of the H3 block: the default route
+    (h3serve/native_engine/model/fused_mlp.py:396-426) runs
+    ``int8_linear(raw, W2, s2, b2, dtype, convrot=True, convrot_groupsize=256,
+    input_act="swiglu")`` and then ``residual[seg].addcmul_(projected[seg],
+    gate[row].to(dtype))`` per modulation segment (layers.py:937-953); here the
+    quantizer is one kernel and the GEMM applies the gated update in its
+    epilogue, so the projection never reaches HBM. ``gate_rows`` is the int32
+    segment-row map of the tokens (fused_mlp.py:34-55). Returns ``residual``."""
+    act = _act_code(input_act)
+    if convrot:
+        why = _convrot_supported(x, act, convrot_groupsize)
+        if why is not None:
+            raise NotImplementedError(f"ConvRot online rotation: {why}")
+    if residual.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("the gated residual must be bf16 or fp16")
+    n = weight.shape[0]
+    k_act = x.shape[-1] // (2 if act == 2 else 1)
+    if k_act != weight.shape[-1]:
+        raise ValueError(
+            f"Input and weight inner dimensions must match, got {k_act} and {weight.shape[-1]}")
+    rows = x.reshape(-1, x.shape[-1]).shape[0]
+    res2 = residual.reshape(-1, residual.shape[-1])
+    if tuple(res2.shape) != (rows, n) or res2.stride(-1) != 1:
+        raise ValueError(f"residual must be [{rows}, {n}] with unit column stride, got {tuple(residual.shape)}")
+    if gate.dim() != 2 or gate.shape[1] != n:
+        raise ValueError(f"gate must be [rows, {n}], got {tuple(gate.shape)}")
+    if gate_rows.numel() != rows:
+        raise ValueError(f"gate_rows must hold one row index per token ({rows}), got {gate_rows.numel()}")
+    if n % 4 or res2.stride(0) % 4:
+        raise NotImplementedError("gated residual epilogue: the output width and residual row stride must be "
+                                  "multiples of 4")
+    g = gate if gate.dtype in (torch.float32, residual.dtype) else gate.to(torch.float32)
+    g = g.to(device=x.device)
+    if g.stride(-1) != 1 or g.stride(0) % 4 or g.data_ptr() % 16:
+        g = g.contiguous()
+    # out-of-range rows are clamped by the kernel (no host sync to check them)
+    gr = gate_rows.to(device=x.device, dtype=torch.int32).reshape(-1).contiguous()
+    if gate.shape[0] < 1:
+        raise ValueError("the gate table needs at least one row")
+    weight = weight.to(device=x.device).contiguous()
+    ws = weight_scale.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
+    if ws.numel() not in (1, n):
+        raise ValueError(
+            f"INT8 weight scale must be scalar or per-output-channel, got {tuple(weight_scale.shape)} "
+            f"for weight shape {tuple(weight.shape)}")
+    if convrot:
+        q, sx = _quantize_convrot(x.reshape(-1, x.shape[-1]), act, convrot_groupsize)
+    else:
+        q, sx = _quantize(x.reshape(-1, x.shape[-1]), act)
+    m, k = q.shape
+    if k % 16:
+        kp = (k + 15) // 16 * 16
+        q = torch.nn.functional.pad(q, (0, kp - k))
+        weight = torch.nn.functional.pad(weight, (0, kp - k))
+        k = kp
+    if bias is not None:
+        bias = bias.to(device=x.device, dtype=residual.dtype).contiguous().reshape(-1)
+    if m and n:
+        call("xmh3_int8_gemm_gated_residual", q.data_ptr(), q.stride(0), weight.data_ptr(), weight.stride(0),
+             m, n, k, sx.data_ptr(), ws.data_ptr(), int(ws.numel() != 1), ptr(bias), res2.data_ptr(),
+             DTYPE_CODE[residual.dtype], res2.stride(0), g.data_ptr(), DTYPE_CODE[g.dtype], g.stride(0),
+             g.shape[0], gr.data_ptr(), stream_of(q))
+    return residual
+
+
 # --------------------------------------------------------------------------- W4A8
 
 def validate_w4a8_operands(qdata, s_rel, s_channel, codebook, correction, group_size, convrot_groupsize):

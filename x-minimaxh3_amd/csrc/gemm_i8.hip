@@ -9,6 +9,13 @@
 //                 atomically fold max|g| per row into row_amax (fp32 bits) --
 //                 fc1 of the fused MLP, feeding the per-token requant of fc2
 //   EPI_INT32   : raw int32 accumulators (parity of the contraction itself)
+//   EPI_GATED   : y = T(...as EPI_DEQUANT...); residual[m,n] =
+//                 T(residual[m,n] + y * T(gate[gate_rows[m], n])) in place --
+//                 fc2 of the H3 block with its AdaLN-gated residual update
+//                 (h3serve/native_engine/model/fused_mlp.py:396-426,
+//                 layers.py:937-953: int8_linear, then addcmul_ per segment;
+//                 the product of two 16-bit floats is exact in fp32, so the
+//                 only rounding before T is the add)
 //
 // Tiling: 256x256 block tile, 4 waves in a 2x2 grid, each wave owning a
 // 128x128 sub-tile held as 8x8 accumulators of v_mfma_i32_16x16x64_i8 (256
@@ -37,7 +44,7 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-enum Epi : int { EPI_DEQUANT = 0, EPI_GELU = 1, EPI_INT32 = 2 };
+enum Epi : int { EPI_DEQUANT = 0, EPI_GELU = 1, EPI_INT32 = 2, EPI_GATED = 3 };
 
 struct GemmArgs {
   const int8_t* A;
@@ -52,6 +59,12 @@ struct GemmArgs {
   int64_t ldo;       // elements
   uint32_t* row_amax;
   int tiles_m, tiles_n;
+  // EPI_GATED: out is the residual (read and written in place)
+  const void* gate;            // [rows, N]: fp32 or the output dtype
+  int64_t ldg;                 // elements
+  int gate_f32;
+  const int32_t* gate_rows;    // [M], clamped into [0, gate_nrows)
+  int gate_nrows;
 };
 
 #ifndef XMH3_GROUP_M
@@ -202,15 +215,85 @@ __device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][
   });
 }
 
+// EPI_GATED: the residual and gate values of row block I+1 are fetched while
+// block I is computed and stored (the residual is read and written by the
+// same lane, so its loads are issued explicitly ahead of the stores rather
+// than left to the compiler, which cannot move loads above stores to the same
+// buffer). Host contract: N, ldo and ldg are multiples of 4 and the residual
+// and gate rows 8- (16- for an fp32 gate) byte aligned, so every column block
+// of 4 is one vector load; rows and columns past the end are clamped for the
+// loads and not stored.
+template <typename TO, bool BIAS, int NI, int NJ>
+__device__ __forceinline__ void epilogue_gated(const GemmArgs& p, v4i (&acc)[NI][NJ], const EpiScalesT<NI, NJ>& sc,
+                                               int row0, int col0, int lane) {
+  using S = typename TO::storage;
+  const int em = row0 + (lane & 15);
+  const int en = col0 + 4 * (lane >> 4);
+  S* const res_base = static_cast<S*>(p.out);
+  const S* const brow = static_cast<const S*>(p.bias);
+  uint2 res[2][NJ];
+  float gt[2][NJ][4];
+  auto fetch = [&](auto I) __attribute__((always_inline)) {
+    constexpr int i = I, b = i & 1;
+    const int m = min(em + i * 16, p.M - 1);
+    const int64_t grow = min(max(p.gate_rows[m], 0), p.gate_nrows - 1);
+    const S* rrow = res_base + (int64_t)m * p.ldo;
+    static_for<NJ>([&](auto J) {
+      constexpr int j = J;
+      const int n = min(en + j * 16, p.N - 4);
+      res[b][j] = *reinterpret_cast<const uint2*>(rrow + n);
+      if (p.gate_f32) {
+        const float4 g4 = *reinterpret_cast<const float4*>(static_cast<const float*>(p.gate) + grow * p.ldg + n);
+        gt[b][j][0] = g4.x; gt[b][j][1] = g4.y; gt[b][j][2] = g4.z; gt[b][j][3] = g4.w;
+      } else {
+        const uint2 g2 = *reinterpret_cast<const uint2*>(static_cast<const S*>(p.gate) + grow * p.ldg + n);
+        gt[b][j][0] = TO::load(g2.x & 0xffffu); gt[b][j][1] = TO::load(g2.x >> 16);
+        gt[b][j][2] = TO::load(g2.y & 0xffffu); gt[b][j][3] = TO::load(g2.y >> 16);
+      }
+    });
+  };
+  fetch(std::integral_constant<int, 0>{});
+  static_for<NI>([&](auto I) {
+    constexpr int i = I, b = i & 1;
+    if constexpr (i + 1 < NI) fetch(std::integral_constant<int, i + 1>{});
+    const int m = em + i * 16;
+    const bool mok = m < p.M;
+    const float sxm = sc.sx[i];
+    S* orow = res_base + (int64_t)m * p.ldo;
+    static_for<NJ>([&](auto J) {
+      constexpr int j = J;
+      const int n = en + j * 16;
+      const uint32_t rw[2] = {res[b][j].x, res[b][j].y};
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float y = TO::round((float)acc[i][j][r] * (sxm * sc.sw[j][r]));
+        if constexpr (BIAS) y = TO::round(y + TO::load(brow[min(n + r, p.N - 1)]));
+        const float g = TO::round(gt[b][j][r]);
+        const float rv = TO::load((rw[r >> 1] >> (16 * (r & 1))) & 0xffffu);
+        v[r] = TO::round(rv + y * g);
+      }
+      if (mok && n < p.N) store4(orow + n, v, TO{});
+    });
+  });
+}
+
 // The bias test is hoisted out of the element loop (a uniform branch per
 // element otherwise).
 template <int EPI, typename TO, bool VEC_OUT, int NI, int NJ>
 __device__ __forceinline__ void epilogue_t(const GemmArgs& p, v4i (&acc)[NI][NJ], const EpiScalesT<NI, NJ>& sc,
                                            int row0, int col0, int lane) {
-  if (EPI != EPI_INT32 && p.bias)
-    epilogue_body<EPI, TO, VEC_OUT, true, NI, NJ>(p, acc, sc, row0, col0, lane);
-  else
-    epilogue_body<EPI, TO, VEC_OUT, false, NI, NJ>(p, acc, sc, row0, col0, lane);
+  if constexpr (EPI == EPI_GATED) {
+    if (p.bias)
+      epilogue_gated<TO, true, NI, NJ>(p, acc, sc, row0, col0, lane);
+    else
+      epilogue_gated<TO, false, NI, NJ>(p, acc, sc, row0, col0, lane);
+  } else {
+    if (EPI != EPI_INT32 && p.bias)
+      epilogue_body<EPI, TO, VEC_OUT, true, NI, NJ>(p, acc, sc, row0, col0, lane);
+    else
+      epilogue_body<EPI, TO, VEC_OUT, false, NI, NJ>(p, acc, sc, row0, col0, lane);
+  }
 }
 
 template <int EPI, typename TO, bool VEC_OUT>
@@ -643,23 +726,26 @@ static int launch_gemm_T(GemmArgs& a, bool vec, hipStream_t st) {
 #ifndef XMH3_GEMM_V5
 #define XMH3_GEMM_V5 1
 #endif
+  // the gated epilogue always has aligned vector rows (host contract): its
+  // scalar-row variants are not instantiated
+  constexpr bool only_vec = EPI == EPI_GATED;
   if (XMH3_GEMM_V5 && a.K % (2 * V5_BK) == 0 && spans_ok) {
-    if (vec)
+    if (vec || only_vec)
       hipLaunchKernelGGL((gemm_i8_v5_kernel<EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
-    else
+    else if constexpr (!only_vec)
       hipLaunchKernelGGL((gemm_i8_v5_kernel<EPI, TO, false>), grid, dim3(NTHREADS), 0, st, a);
     return check_launch("gemm_i8_v5_kernel");
   }
   if (a.K % (2 * DMA_BK) == 0 && spans_ok) {
-    if (vec)
+    if (vec || only_vec)
       hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
-    else
+    else if constexpr (!only_vec)
       hipLaunchKernelGGL((gemm_i8_dma_kernel<EPI, TO, false>), grid, dim3(NTHREADS), 0, st, a);
     return check_launch("gemm_i8_dma_kernel");
   }
-  if (vec)
+  if (vec || only_vec)
     hipLaunchKernelGGL((gemm_i8_kernel<BK, EPI, TO, true>), grid, dim3(NTHREADS), 0, st, a);
-  else
+  else if constexpr (!only_vec)
     hipLaunchKernelGGL((gemm_i8_kernel<BK, EPI, TO, false>), grid, dim3(NTHREADS), 0, st, a);
   return check_launch("gemm_i8_kernel");
 }
@@ -688,6 +774,7 @@ int int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_
   a.M = (int)M; a.N = (int)N; a.K = (int)K;
   a.sx = sx; a.sw = sw; a.sw_per_channel = sw_per_channel;
   a.bias = bias; a.out = out; a.ldo = ldo; a.row_amax = row_amax;
+  a.gate = nullptr; a.ldg = 0; a.gate_f32 = 0; a.gate_rows = nullptr; a.gate_nrows = 0;
   a.tiles_m = (int)((M + BM - 1) / BM);
   a.tiles_n = (int)((N + BN - 1) / BN);
   XMH3_REQUIRE((int64_t)a.tiles_m * a.tiles_n < (1LL << 31), "int8_gemm: grid too large");
@@ -709,6 +796,42 @@ int int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_
   }
 }
 
+int int8_gemm_gated(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, int64_t M, int64_t N,
+                    int64_t K, const float* sx, const float* sw, int sw_per_channel, const void* bias,
+                    void* residual, int res_dtype, int64_t ldr, const void* gate, int gate_dtype, int64_t ldg,
+                    int64_t gate_nrows, const int32_t* gate_rows, hipStream_t st) {
+  XMH3_REQUIRE(M >= 0 && N >= 0 && K >= 0, "int8_gemm_gated_residual: negative size");
+  XMH3_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), "int8_gemm_gated_residual: size too large");
+  if (M == 0 || N == 0) return XMH3_OK;
+  XMH3_REQUIRE(A && B && residual && sx && sw && gate && gate_rows, "int8_gemm_gated_residual: null operand");
+  XMH3_REQUIRE(gate_nrows >= 1 && gate_nrows < (1LL << 31), "int8_gemm_gated_residual: gate table needs >= 1 row");
+  XMH3_REQUIRE(K % 16 == 0, "int8_gemm_gated_residual: K must be a multiple of 16");
+  XMH3_REQUIRE(lda % 16 == 0 && ldb % 16 == 0 && lda >= K && ldb >= K,
+               "int8_gemm_gated_residual: row strides must be multiples of 16 bytes and >= K");
+  XMH3_REQUIRE((uintptr_t)A % 16 == 0 && (uintptr_t)B % 16 == 0,
+               "int8_gemm_gated_residual: operands must be 16-byte aligned");
+  XMH3_REQUIRE(K <= 131072, "int8_gemm_gated_residual: K > 131072 could overflow int32 accumulators");
+  XMH3_REQUIRE(res_dtype == DT_BF16 || res_dtype == DT_F16, "int8_gemm_gated_residual: residual must be bf16 or fp16");
+  XMH3_REQUIRE(gate_dtype == DT_F32 || gate_dtype == res_dtype,
+               "int8_gemm_gated_residual: gate must be fp32 or the residual's dtype");
+  XMH3_REQUIRE(N % 4 == 0 && ldr % 4 == 0 && ldr >= N && ldg % 4 == 0 && ldg >= N,
+               "int8_gemm_gated_residual: N and the residual / gate row strides must be multiples of 4");
+  XMH3_REQUIRE((uintptr_t)residual % 8 == 0 && (uintptr_t)gate % (gate_dtype == DT_F32 ? 16 : 8) == 0,
+               "int8_gemm_gated_residual: residual / gate rows must be 8-byte (fp32 gate: 16-byte) aligned");
+  GemmArgs a;
+  a.A = A; a.B = B; a.lda = lda; a.ldb = ldb;
+  a.M = (int)M; a.N = (int)N; a.K = (int)K;
+  a.sx = sx; a.sw = sw; a.sw_per_channel = sw_per_channel;
+  a.bias = bias; a.out = residual; a.ldo = ldr; a.row_amax = nullptr;
+  a.gate = gate; a.ldg = ldg; a.gate_f32 = gate_dtype == DT_F32; a.gate_rows = gate_rows;
+  a.gate_nrows = (int)gate_nrows;
+  a.tiles_m = (int)((M + BM - 1) / BM);
+  a.tiles_n = (int)((N + BN - 1) / BN);
+  XMH3_REQUIRE((int64_t)a.tiles_m * a.tiles_n < (1LL << 31), "int8_gemm_gated_residual: grid too large");
+  if (res_dtype == DT_BF16) return launch_gemm_T<128, EPI_GATED, BF16T>(a, true, st);
+  return launch_gemm_T<128, EPI_GATED, F16T>(a, true, st);
+}
+
 #endif  // XMH3_GEMM_KERNELS_ONLY
 }  // namespace xmh3
 
@@ -720,5 +843,14 @@ extern "C" int xmh3_int8_gemm(const int8_t* A, int64_t lda, const int8_t* B, int
                               hipStream_t stream) {
   return xmh3::int8_gemm(A, lda, B, ldb, M, N, K, sx, sw, sw_per_channel, bias, out, out_dtype, ldo,
                          epilogue, row_absmax_bits, stream);
+}
+
+extern "C" int xmh3_int8_gemm_gated_residual(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb,
+                                             int64_t M, int64_t N, int64_t K, const float* sx, const float* sw,
+                                             int sw_per_channel, const void* bias, void* residual, int res_dtype,
+                                             int64_t ldr, const void* gate, int gate_dtype, int64_t ldg,
+                                             int64_t gate_nrows, const int32_t* gate_rows, hipStream_t stream) {
+  return xmh3::int8_gemm_gated(A, lda, B, ldb, M, N, K, sx, sw, sw_per_channel, bias, residual, res_dtype, ldr,
+                               gate, gate_dtype, ldg, gate_nrows, gate_rows, stream);
 }
 #endif

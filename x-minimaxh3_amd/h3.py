@@ -10,6 +10,11 @@
 * ``apply_qknorm_rope(query, key, *, q_weight, k_weight, frequencies, eps)``
   is the table form of h3serve/native_engine/model/layers.py:72-100.
 * ``segment_row_map`` follows h3serve/native_engine/model/fused_mlp.py:34-55.
+* ``fused_down_gated_residual`` has the signature of
+  h3serve/native_engine/model/fused_mlp.py:157-165 (SwiGLU + ConvRot
+  quantizer, fc2 GEMM with the gated residual update in its epilogue), and
+  ``gated_swiglu_mlp_`` is the int8 route of ``try_fused_gated_mlp``
+  (fused_mlp.py:269-426) over token chunks.
 """
 
 from __future__ import annotations
@@ -88,3 +93,39 @@ def mi355x_w4a8_kernel(value, qdata, s_rel, s_channel, codebook, correction, bia
     return ops.w4a8_int8_linear(value, qdata, s_rel, s_channel, codebook=codebook, correction=correction,
                                 bias=bias, group_size=group_size, convrot_groupsize=convrot_group_size or 256,
                                 out_dtype=output_dtype, convrot=bool(convrot_group_size))
+
+
+def fused_down_gated_residual(hidden: torch.Tensor, residual: torch.Tensor, gate: torch.Tensor,
+                              gate_rows: torch.Tensor, qweight: torch.Tensor, weight_scale: torch.Tensor,
+                              bias: torch.Tensor | None) -> None:
+    """residual += fc2(swiglu(hidden)) * gate[gate_rows], in place: ``hidden``
+    is the raw fc1 output ``[rows, 2 * ffn]`` ([gate | up]), ``qweight`` the
+    ConvRot-rotated int8 fc2 weight, ``gate_rows`` the int32 segment-row map of
+    the rows (fused_mlp.py:157-222)."""
+    backend.int8_linear_gated_residual_(hidden.reshape(-1, hidden.shape[-1]), qweight, weight_scale, bias,
+                                        residual, gate, gate_rows, convrot=True, convrot_groupsize=256,
+                                        input_act="swiglu")
+
+
+def gated_swiglu_mlp_(residual: torch.Tensor, hidden: torch.Tensor, fc1_qweight: torch.Tensor,
+                      fc1_scale: torch.Tensor, fc1_bias: torch.Tensor | None, fc2_qweight: torch.Tensor,
+                      fc2_scale: torch.Tensor, fc2_bias: torch.Tensor | None, gate: torch.Tensor, segments,
+                      *, chunk_tokens: int = 8192) -> torch.Tensor:
+    """The int8 route of ``try_fused_gated_mlp`` (fused_mlp.py:340-426): per
+    chunk of tokens, raw = fc1(hidden) (ConvRot int8 linear), then the fused
+    SwiGLU + ConvRot quantizer and fc2 with the gated residual update. Both
+    weights are the checkpoint's rotated int8 ones. Updates ``residual`` in
+    place and returns it."""
+    if chunk_tokens <= 0:
+        raise ValueError("MLP chunk_tokens must be positive")
+    if hidden.ndim != 2:
+        raise ValueError("hidden must be [tokens, width]")
+    rows = segment_row_map(hidden.shape[0], segments, hidden.device)
+    for start in range(0, hidden.shape[0], chunk_tokens):
+        stop = min(start + chunk_tokens, hidden.shape[0])
+        raw = ops.int8_linear(hidden[start:stop], fc1_qweight, fc1_scale, fc1_bias, hidden.dtype, convrot=True,
+                              convrot_groupsize=256)
+        backend.int8_linear_gated_residual_(raw, fc2_qweight, fc2_scale, fc2_bias, residual[start:stop], gate,
+                                            rows[start:stop], convrot=True, convrot_groupsize=256,
+                                            input_act="swiglu")
+    return residual
