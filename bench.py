@@ -11,7 +11,10 @@ starts):
   * W4A8 MLP at the same shape (group-128 int4 weights decoded on the GPU);
   * the long 16x68x120 grid (M=130560): norm-rope + W8A8 MLP in 16384-token
     chunks, HBM-resident (compute rate) and streamed from pinned host memory
-    through double-buffered device slots (end-to-end, PCIe included).
+    through double-buffered device slots (end-to-end, PCIe included);
+  * the SwiGLU + ConvRot-256 row quantizer on H3's fc2 input (25200 x 14336)
+    and H3's fc2 with the gated residual update in the GEMM epilogue (d=5376),
+    against the same kernels with a separate addcmul_.
 
 A step is one pass of the MLP block over the batch. The timed region runs the
 four MLP kernels (per-token quant, fc1 GEMM + dequant/GELU/row-amax epilogue,
@@ -154,6 +157,41 @@ def bench_convrot(pkg, dev, steps: int, warmup: int) -> dict:
             "algorithmic": "(5*ffn + 4) bytes per token: [gate | up] bf16 read, int8 codes + fp32 scale written"}
 
 
+def bench_h3_fc2(pkg, dev, steps: int, warmup: int) -> dict:
+    """The H3 block's fc2 boundary at the 720p token count with H3's widths
+    (d=5376, ffn=14336): SwiGLU + ConvRot quantizer, then fc2 with the gated
+    residual update in the GEMM epilogue, against the same kernels with the
+    update as a separate torch addcmul_ (the reference's default route)."""
+    import torch
+
+    from x_minimaxh3_amd import backend
+
+    m, d, f = 25200, 5376, 14336
+    g = torch.Generator(device=dev).manual_seed(4)
+    raw = torch.randn(m, 2 * f, device=dev, generator=g).bfloat16()
+    w2 = torch.randint(-127, 128, (d, f), device=dev, generator=g, dtype=torch.int8)
+    s2 = torch.rand(d, device=dev, generator=g) * 1e-3 + 1e-4
+    res = torch.randn(m, d, device=dev, generator=g).bfloat16()
+    gate = torch.randn(1, d, device=dev, generator=g) * 0.1
+    rows = torch.zeros(m, dtype=torch.int32, device=dev)
+
+    def fused():
+        backend.int8_linear_gated_residual_(raw, w2, s2, None, res, gate, rows, convrot=True, input_act="swiglu")
+
+    def unfused():
+        y = backend.int8_linear(raw, w2, s2, None, torch.bfloat16, convrot=True, input_act="swiglu")
+        res.addcmul_(y, gate[0].to(torch.bfloat16))
+
+    ms_f = timed(fused, steps, warmup)
+    ms_u = timed(unfused, steps, warmup)
+    tops = 2.0 * m * d * f / (ms_f * 1e-3) / 1e12
+    return {"workload": "h3_fc2_gated_720p", "tokens": m, "d_model": d, "ffn": f,
+            "ms_fused": round(ms_f, 4), "ms_unfused": round(ms_u, 4), "value": round(tops, 2), "unit": "TOPS",
+            "frac_of_peak": round(tops / PEAK_INT8_TOPS, 4),
+            "note": "SwiGLU+ConvRot quantizer + fc2 GEMM with the gated residual in its epilogue; "
+                    "unfused = same kernels with a bf16 projection and torch addcmul_"}
+
+
 def bench_long(pkg, dev, inp: dict, warmup: int) -> dict:
     import torch
 
@@ -210,7 +248,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the W4A8 and long-sequence measurements")
+    ap.add_argument("--no-extra", action="store_true", help="skip the W4A8, long-sequence, ConvRot and H3 fc2 measurements")
     ap.add_argument("--cpu-sample-rows", type=int, default=0, help="tokens of the CPU baseline (0 = all)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run one 1 GiB device-to-device copy (reference for HBM byte counters)")
@@ -322,12 +360,15 @@ def main() -> int:
     log(f"norm_rope: {nr_ms * 1e3:.1f} us/launch, {nr_gbs:.0f} GB/s ({nr_gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
     # ------------------------------------------------------------------ W4A8 and long sequence
-    w4 = long = cr = None
+    w4 = long = cr = h3fc2 = None
     if not args.no_extra:
         w4 = bench_w4a8(pkg, dev, max(3, args.steps // 4), 2)
         log(f"w4a8 mlp: {w4['ms_per_step']:.3f} ms/step ({w4['value']} TOPS)")
         cr = bench_convrot(pkg, dev, args.steps, args.warmup)
         log(f"convrot swiglu quant: {cr['us_per_launch']:.1f} us/launch, {cr['achieved']:.0f} GB/s")
+        h3fc2 = bench_h3_fc2(pkg, dev, max(3, args.steps // 2), 2)
+        log(f"h3 fc2 gated: fused {h3fc2['ms_fused']:.3f} ms ({h3fc2['value']} TOPS), "
+            f"unfused {h3fc2['ms_unfused']:.3f} ms")
         long = bench_long(pkg, dev, inp, args.warmup)
         log(f"long: resident {long['resident_ms']:.2f} ms ({long['resident_mlp_tops']} MLP TOPS), "
             f"streamed {long['streamed_ms']:.2f} ms ({long['streamed_host_gbs']} GB/s of host I/O), "
@@ -376,6 +417,7 @@ def main() -> int:
                       "algorithmic": "8*M*d bytes (Q,K read + written, bf16)"},
         "w4a8_mlp": w4,
         "convrot_quant": cr,
+        "h3_fc2_gated": h3fc2,
         "long": long,
         "cpu_baseline": cpu,
         "cpu_baseline_norm_rope": cpu_nr,
