@@ -126,6 +126,20 @@ int xmh3_int8_gemm_gated_residual(const int8_t* A, int64_t lda, const int8_t* B,
                                   const int32_t* gate_rows, xmh3_stream_t stream);
 
 /*
+ * Operand of the asymmetric W4A8 correction:
+ *   out[m, g] = T(T(sum of q[m, g*gs .. g*gs+gs-1]) * T(xs[m]))
+ * (T = out_dtype: 0 fp32, 1 fp16, 2 bf16); the caller then adds
+ * out @ T(correction) [groups, N] to the int8 linear's output.
+ * q: int8 [M, ldq] (16-byte aligned rows when gs % 16 == 0); xs: fp32 [M];
+ * out: [M, ldo], ldo >= K / gs.
+ * Replaces: the group-sum step of CK/backends/cuda/__init__.py:2294-2297
+ *   sx = xq.view(m, groups, group_size).sum(-1, dtype=int32).to(out_dtype)
+ *   sx = sx * xs.to(out_dtype)
+ */
+int xmh3_int8_group_sums(const int8_t* q, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                         int64_t group_size, void* out, int out_dtype, int64_t ldo, xmh3_stream_t stream);
+
+/*
  * Grouped int4 -> int8 grid decode (low nibble = even k).
  * Replaces: CK/backends/cuda/ops/w4a8_gemm.cu:94
  *   launch_dequant_int4_grouped_to_int8(qw, s_rel, codebook, out, N, K, G, stream)

@@ -335,6 +335,38 @@ def w4a8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor,
                        convrot=convrot, convrot_groupsize=convrot_groupsize)
 
 
+def int8_group_sums(q: torch.Tensor, xs: torch.Tensor, group_size: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """CK/backends/cuda/__init__.py:2294-2296: the per-group sums of the
+    activation codes in out_dtype, times the row scale in out_dtype."""
+    m, k = q.shape
+    sx = q.view(m, k // group_size, group_size).sum(-1, dtype=torch.int32).to(out_dtype)
+    return sx * xs.reshape(m, 1).to(out_dtype)
+
+
+def w4a8_linear_h3(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, s_channel: torch.Tensor,
+                   codebook: torch.Tensor | None = None, correction: torch.Tensor | None = None,
+                   bias: torch.Tensor | None = None, group_size: int = 16, convrot_groupsize: int = 256,
+                   out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """The H3 checkpoint form of w4a8_int8_linear (group 16, fp8 s_rel, codebook,
+    ConvRot, asymmetric correction), as the reference's GPU dispatcher runs it
+    (CK/backends/cuda/__init__.py:2164-2298): ConvRot row quantizer, codebook
+    decode to the int8 grid, int8 linear with s_channel, and with a correction
+    out.addmm_(int8_group_sums(q, xs), correction.to(out_dtype)). (The eager
+    reference, CK/backends/eager/w4a8_int8.py:457-491, takes the asymmetric
+    case through a floating dequantised weight instead; the two agree to the
+    activation quantization error.)"""
+    lead = x.shape[:-1]
+    k = x.shape[-1]
+    x2 = rotate_activation(x.reshape(-1, k), convrot_groupsize)
+    q, xs = quantize_int8_rowwise(x2)
+    w8 = dequant_int4_grouped_to_int8(qdata, s_rel.float(), group_size, codebook=codebook)
+    ws = s_channel.to(torch.float32).reshape(-1)
+    out = dequant(int8_mm(q, w8), xs, ws, out_dtype, bias)
+    if correction is not None:
+        out.addmm_(int8_group_sums(q, xs, group_size, out_dtype), correction.to(out_dtype))
+    return out.reshape(*lead, qdata.shape[0])
+
+
 def w4a8_mlp(x, w1_packed, w1_srel, w1_sch, w2_packed, w2_srel, w2_sch, group_size=128):
     h = w4a8_linear(x, w1_packed, w1_srel, w1_sch, group_size)
     return w4a8_linear(h, w2_packed, w2_srel, w2_sch, group_size, input_act="gelu_tanh")

@@ -689,3 +689,62 @@ def test_h3_gated_swiglu_mlp(pkg, dev):
                          s2.reshape(-1).to(dev), None, gate.to(dev), segments, chunk_tokens=128)
     torch.cuda.synchronize()
     close(got, want, "h3 gated swiglu mlp")
+
+
+@pytest.mark.parametrize("gs", [16, 8, 32])
+def test_int8_group_sums(pkg, dev, gs):
+    say(f"int8 group sums gs={gs}")
+    from x_minimaxh3_amd._lib import DTYPE_CODE, call, stream_of
+
+    g = torch.Generator().manual_seed(gs)
+    m, k = 203, 1536
+    q = torch.randint(-128, 128, (m, k), generator=g, dtype=torch.int8)
+    q[7] = -128
+    q[8] = 127
+    xs = torch.rand(m, 1, generator=g) * 0.05
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        out = torch.empty(m, k // gs, dtype=dt, device=dev)
+        qd, xsd = q.to(dev), xs.to(dev)
+        call("xmh3_int8_group_sums", qd.data_ptr(), qd.stride(0), xsd.data_ptr(), m, k, gs, out.data_ptr(),
+             DTYPE_CODE[dt], out.stride(0), stream_of(qd))
+        torch.cuda.synchronize()
+        assert same(out, cpu_ref.int8_group_sums(q, xs, gs, dt), f"group sums {dt}")
+
+
+def test_w4a8_h3_checkpoint_format(pkg, dev):
+    """The H3 W4A8 layout end to end: group 16, fp8-e4m3 s_rel, the
+    Lloyd-Max codebook, ConvRot and the asymmetric correction, with a bias,
+    through the checkpoint loader."""
+    say("w4a8 H3 checkpoint format (group 16, e4m3 s_rel, codebook, correction)")
+    from x_minimaxh3_amd import h3
+
+    g = torch.Generator().manual_seed(9)
+    m, n, k, gs = 300, 640, 1536, 16
+    lut = torch.tensor([-0.980602, -0.794529, -0.638165, -0.500986, -0.377321, -0.263187, -0.155210,
+                        -0.050720, 0.052541, 0.156985, 0.265284, 0.379533, 0.502636, 0.638953, 0.794876,
+                        0.980671])
+    tensors = {
+        "fc.weight": torch.randint(-128, 128, (n, k // 2), generator=g, dtype=torch.int8),
+        "fc.weight_s_rel": (torch.rand(n, k // gs, generator=g) * 90 + 30).to(torch.float8_e4m3fn),
+        "fc.weight_s_channel": torch.rand(n, generator=g) * 2e-4 + 1e-4,
+        "fc.weight_codebook": lut,
+        "fc.weight_correction": torch.randn(k // gs, n, generator=g) * 2e-3,
+        "fc.bias": torch.randn(n, generator=g) * 0.1,
+    }
+    x = outlier_acts(m, k, seed=10)
+    lin = h3.load_w4a8_linear({key: t.to(dev) for key, t in tensors.items()}, "fc")
+    y = lin(x.to(dev))
+    torch.cuda.synchronize()
+    yr = cpu_ref.w4a8_linear_h3(x, tensors["fc.weight"], tensors["fc.weight_s_rel"],
+                                tensors["fc.weight_s_channel"], codebook=lut,
+                                correction=tensors["fc.weight_correction"], bias=tensors["fc.bias"],
+                                group_size=gs, out_dtype=torch.bfloat16)
+    close(y, yr, "w4a8 h3 format")
+    # without the correction the int8 part alone
+    lin0 = h3.load_w4a8_linear({key: t.to(dev) for key, t in tensors.items() if "correction" not in key}, "fc")
+    y0 = lin0(x.to(dev))
+    torch.cuda.synchronize()
+    y0r = cpu_ref.w4a8_linear_h3(x, tensors["fc.weight"], tensors["fc.weight_s_rel"],
+                                 tensors["fc.weight_s_channel"], codebook=lut, bias=tensors["fc.bias"],
+                                 group_size=gs, out_dtype=torch.bfloat16)
+    close(y0, y0r, "w4a8 h3 format, no correction")

@@ -377,3 +377,38 @@ def test_gated_residual_closed_form_and_row_map():
         cpu_ref.segment_row_map(m, ((0, 40, 0), (41, 97, 1)))
     with pytest.raises(ValueError):
         cpu_ref.gated_residual_(res.clone(), upd, gate, ((0, 50, 0),))
+
+
+def test_w4a8_correction_route_against_float_weight():
+    """The GPU dispatcher's asymmetric route (int8 linear + group sums of the
+    codes times the correction) against the eager float route
+    (CK/backends/eager/w4a8_int8.py:405-491: W = rotate(w8 * s_channel +
+    correction), x @ W^T): equal up to the activation quantization error, and
+    a transposed or dropped correction is far off."""
+    g = torch.Generator().manual_seed(5)
+    m, n, k, gs = 48, 96, 512, 16
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    codes = torch.randint(-128, 128, (n, k // 2), generator=g, dtype=torch.int8)
+    srel = (torch.rand(n, k // gs, generator=g) * 80 + 40).to(torch.float8_e4m3fn)
+    sch = torch.rand(n, generator=g) * 2e-3 + 1e-3
+    cb = torch.linspace(-0.98, 0.98, 16)
+    corr = torch.randn(k // gs, n, generator=g) * 0.05
+    got = cpu_ref.w4a8_linear_h3(x, codes, srel, sch, codebook=cb, correction=corr, group_size=gs,
+                                 out_dtype=torch.float32)
+    w8 = cpu_ref.dequant_int4_grouped_to_int8(codes, srel.float(), gs, codebook=cb).double()
+    w_rot = (w8.view(n, k // gs, gs) * sch.double().view(n, 1, 1) + corr.double().T.unsqueeze(-1)).view(n, k)
+    h = cpu_ref.build_hadamard(256).double()
+    w_phys = (w_rot.view(n, k // 256, 256) @ h).view(n, k)
+    want = x.double() @ w_phys.T
+    cos = torch.nn.functional.cosine_similarity(got.double().flatten(), want.flatten(), dim=0).item()
+    assert cos > 0.9999
+    no_corr = cpu_ref.w4a8_linear_h3(x, codes, srel, sch, codebook=cb, group_size=gs, out_dtype=torch.float32)
+    assert torch.nn.functional.cosine_similarity(no_corr.double().flatten(), want.flatten(), dim=0).item() < 0.999
+    # group sums: brute force
+    q = torch.randint(-128, 128, (5, 64), generator=g, dtype=torch.int8)
+    xs = torch.rand(5, 1, generator=g)
+    sums = cpu_ref.int8_group_sums(q, xs, 16, torch.float32)
+    for r in range(5):
+        for grp in range(4):
+            total = torch.tensor(float(int(q[r, 16 * grp:16 * grp + 16].int().sum())))
+            assert sums[r, grp].item() == (total * xs[r, 0]).item()      # one fp32 product

@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple] = {
     "xmh3_int8_gemm_gated_residual": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p,
                                               c_void_p, c_int, c_void_p, c_void_p, c_int, c_i64, c_void_p, c_int,
                                               c_i64, c_i64, c_void_p, c_void_p]),
+    "xmh3_int8_group_sums": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_void_p, c_int, c_i64,
+                                     c_void_p]),
     "xmh3_w4_decode_int8": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_i64, c_i64, c_i64, c_void_p, c_void_p]),
     "xmh3_w8a8_mlp_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
     "xmh3_w8a8_mlp": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_int, c_void_p,

@@ -5,9 +5,8 @@ the reference backend function it replaces (CK = backends/turbo/vendor/
 comfy_kitchen): validation raises ``ValueError`` with the reference's
 conditions; work goes to the HIP library on the tensors' current stream; there
 is no CPU path. Features the reference has but this backend does not
-implement (ConvRot rotation, stochastic rounding, swiglu input act, the
-asymmetric W4A8 correction) raise ``NotImplementedError`` instead of returning
-different numbers.
+implement (stochastic rounding, ConvRot groups other than 256) raise
+``NotImplementedError`` instead of returning different numbers.
 """
 
 from __future__ import annotations
@@ -317,15 +316,33 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
     validate_w4a8_operands(qdata, s_rel, s_channel, codebook, correction, group_size, convrot_groupsize)
     if x.shape[-1] != qdata.shape[-1] * 2:
         raise ValueError(f"Input K={x.shape[-1]} does not match qdata K={qdata.shape[-1] * 2}")
-    if correction is not None:
-        raise NotImplementedError("asymmetric W4A8 (correction) is not implemented by the mi355x backend")
     if convrot:
         why = _convrot_supported(x, 0, convrot_groupsize)
         if why is not None:
             raise NotImplementedError(f"ConvRot online rotation: {why}")
     w8 = dequant_int4_grouped_to_int8(qdata, s_rel, codebook, group_size)
-    return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype, convrot=convrot,
-                       convrot_groupsize=convrot_groupsize)
+    if correction is None:
+        return int8_linear(x, w8, s_channel, bias=bias, out_dtype=out_dtype, convrot=convrot,
+                           convrot_groupsize=convrot_groupsize)
+    # asymmetric (the H3 checkpoints): as the reference's GPU dispatcher
+    # (CK/backends/cuda/__init__.py:2164-2298), the int8 linear plus
+    # T(T(group sums of the codes) * T(xs)) @ T(correction)
+    if out_dtype is None:
+        out_dtype = torch.bfloat16
+    k = x.shape[-1]
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, k)
+    q, xs = _quantize_convrot(x2, 0, convrot_groupsize) if convrot else _quantize(x2, 0)
+    ws = s_channel.to(device=x.device, dtype=torch.float32).reshape(-1).contiguous()
+    out = _gemm(q, xs, w8, ws, bias, out_dtype)
+    m = q.shape[0]
+    groups = k // group_size
+    sums = torch.empty(m, groups, dtype=out_dtype, device=x.device)
+    if m:
+        call("xmh3_int8_group_sums", q.data_ptr(), q.stride(0), xs.data_ptr(), m, k, group_size, sums.data_ptr(),
+             DTYPE_CODE[out_dtype], sums.stride(0), stream_of(q))
+        out.addmm_(sums, correction.to(device=x.device, dtype=out_dtype))
+    return out.reshape(*lead, qdata.shape[0])
 
 
 # --------------------------------------------------------------------------- MLP blocks

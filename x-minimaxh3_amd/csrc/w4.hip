@@ -113,7 +113,73 @@ int w4_decode(const uint8_t* packed, const void* s_rel, int s_rel_dtype, const f
   return check_launch("w4_decode_generic_kernel");
 }
 
+// Operand of the asymmetric W4A8 correction (the weight's per-group offset
+// correction[g, n] times the group sums of the activation codes):
+//   s[m, g] = T(T(sum_{k in group g} q[m, k]) * T(xs[m]))
+// as CK/backends/cuda/__init__.py:2294-2297 forms it before its
+// out.addmm_(s, T(correction)). One thread per (row, group).
+__device__ __forceinline__ int sum_bytes(uint32_t w) {
+  return (int)(int8_t)(w & 0xffu) + (int)(int8_t)((w >> 8) & 0xffu) + (int)(int8_t)((w >> 16) & 0xffu) +
+         (int)(int8_t)(w >> 24);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void int8_group_sums_kernel(const int8_t* __restrict__ q, int64_t ldq,
+                                                              const float* __restrict__ xs, int64_t M, int G,
+                                                              int gs, typename T::storage* __restrict__ out,
+                                                              int64_t ldo) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= M * G) return;
+  const int64_t m = t / G;
+  const int g = (int)(t - m * G);
+  const int8_t* p = q + m * ldq + (int64_t)g * gs;
+  int sum = 0;
+  if (gs % 16 == 0) {
+    for (int c = 0; c < gs; c += 16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p + c);
+      sum += sum_bytes(v.x) + sum_bytes(v.y) + sum_bytes(v.z) + sum_bytes(v.w);
+    }
+  } else {
+    for (int c = 0; c < gs; ++c) sum += p[c];
+  }
+  const float v = T::round(T::round((float)sum) * T::round(xs[m]));
+  out[m * ldo + g] = (typename T::storage)T::store(v);
+}
+
+int int8_group_sums(const int8_t* q, int64_t ldq, const float* xs, int64_t M, int64_t K, int64_t gs, void* out,
+                    int out_dtype, int64_t ldo, hipStream_t st) {
+  XMH3_REQUIRE(M >= 0 && K >= 0 && gs > 0, "int8_group_sums: bad sizes");
+  if (M == 0 || K == 0) return XMH3_OK;
+  XMH3_REQUIRE(q && xs && out, "int8_group_sums: null pointer");
+  XMH3_REQUIRE(K % gs == 0 && gs <= 4096, "int8_group_sums: K must be a multiple of group_size (<= 4096)");
+  const int64_t G = K / gs;
+  XMH3_REQUIRE(ldq >= K && ldo >= G && G < (1LL << 31), "int8_group_sums: bad strides");
+  if (gs % 16 == 0)
+    XMH3_REQUIRE(ldq % 16 == 0 && (uintptr_t)q % 16 == 0, "int8_group_sums: rows must be 16-byte aligned");
+  const int64_t threads = M * G;
+  XMH3_REQUIRE((threads + 255) / 256 < (1LL << 31), "int8_group_sums: too many groups");
+  dim3 grid((unsigned)((threads + 255) / 256));
+  if (out_dtype == DT_BF16)
+    hipLaunchKernelGGL(int8_group_sums_kernel<BF16T>, grid, dim3(256), 0, st, q, ldq, xs, M, (int)G, (int)gs,
+                       static_cast<uint16_t*>(out), ldo);
+  else if (out_dtype == DT_F16)
+    hipLaunchKernelGGL(int8_group_sums_kernel<F16T>, grid, dim3(256), 0, st, q, ldq, xs, M, (int)G, (int)gs,
+                       static_cast<uint16_t*>(out), ldo);
+  else if (out_dtype == DT_F32)
+    hipLaunchKernelGGL(int8_group_sums_kernel<F32T>, grid, dim3(256), 0, st, q, ldq, xs, M, (int)G, (int)gs,
+                       static_cast<float*>(out), ldo);
+  else
+    return fail(XMH3_EUNSUPPORTED, "int8_group_sums: out dtype must be fp32, fp16 or bf16");
+  return check_launch("int8_group_sums_kernel");
+}
+
 }  // namespace xmh3
+
+extern "C" int xmh3_int8_group_sums(const int8_t* q, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                                    int64_t group_size, void* out, int out_dtype, int64_t ldo,
+                                    hipStream_t stream) {
+  return xmh3::int8_group_sums(q, ldq, xs, M, K, group_size, out, out_dtype, ldo, stream);
+}
 
 extern "C" int xmh3_w4_decode_int8(const uint8_t* packed, const void* s_rel, int s_rel_dtype,
                                    const float* codebook, int64_t N, int64_t K, int64_t group_size,

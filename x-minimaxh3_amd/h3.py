@@ -15,9 +15,16 @@
   quantizer, fc2 GEMM with the gated residual update in its epilogue), and
   ``gated_swiglu_mlp_`` is the int8 route of ``try_fused_gated_mlp``
   (fused_mlp.py:269-426) over token chunks.
+* ``W4A8QuantSpec`` / ``load_w4a8_linear`` read the H3 W4A8 checkpoint layout
+  (safetensors keys ``weight``, ``weight_s_rel``, ``weight_s_channel``,
+  ``weight_codebook``, ``weight_correction``, ``bias``; quantization.py:153-187,
+  416-516, assembly.py:166-228) into a callable linear on the GPU path.
 """
 
 from __future__ import annotations
+
+from collections.abc import Mapping
+from dataclasses import dataclass
 
 import torch
 
@@ -129,3 +136,90 @@ def gated_swiglu_mlp_(residual: torch.Tensor, hidden: torch.Tensor, fc1_qweight:
                                             rows[start:stop], convrot=True, convrot_groupsize=256,
                                             input_act="swiglu")
     return residual
+
+
+@dataclass(frozen=True)
+class W4A8QuantSpec:
+    """The layout recorded by the H3 mixed W4A8 checkpoints
+    (h3serve/native_engine/model/quantization.py:153-187)."""
+
+    format: str = "asym_w4a8_int8"
+    group_size: int = 16
+    convrot: bool = True
+    convrot_groupsize: int = 256
+
+    @classmethod
+    def from_mapping(cls, data: Mapping[str, object]) -> "W4A8QuantSpec":
+        return cls(format=str(data.get("format", "")), group_size=int(data.get("group_size", 16)),
+                   convrot=bool(data.get("convrot", True)),
+                   convrot_groupsize=int(data.get("convrot_groupsize", 256)))
+
+    def validate_supported(self) -> None:
+        if self.format != "asym_w4a8_int8":
+            raise ValueError(f"native core currently supports asym_w4a8_int8, got {self.format!r}")
+        if self.group_size < 4 or (16 % self.group_size != 0 and self.group_size % 16 != 0):
+            raise ValueError("W4A8 group size must be >=4 and divide 16 or be a multiple of 16")
+        if not self.convrot:
+            raise ValueError("the H3 W4A8 checkpoint requires ConvRot")
+        size = self.convrot_groupsize
+        if size < 4 or size & (size - 1) or size.bit_length() % 2 == 0:
+            raise ValueError("ConvRot group size must be a power of four")
+
+
+class W4A8Linear:
+    """A W4A8 linear in the H3 checkpoint layout, computed by
+    ``w4a8_int8_linear`` (ConvRot row quantizer, codebook / fp8-scale decode
+    to the int8 grid, int8 GEMM, asymmetric correction)."""
+
+    def __init__(self, qdata, s_rel, s_channel, *, codebook=None, correction=None, bias=None,
+                 spec: W4A8QuantSpec = W4A8QuantSpec(), output_dtype: torch.dtype | None = None):
+        spec.validate_supported()
+        if qdata.ndim != 2 or qdata.dtype != torch.int8:
+            raise ValueError("packed W4 weight must be a rank-two int8 tensor")
+        out_features = qdata.shape[0]
+        if bias is not None and bias.numel() != out_features:
+            raise ValueError("bias does not match W4A8 output rows")
+        backend.validate_w4a8_operands(qdata, s_rel, s_channel, codebook, correction, spec.group_size,
+                                       spec.convrot_groupsize)
+        self.qdata, self.s_rel, self.s_channel = qdata, s_rel, s_channel
+        self.codebook, self.correction, self.bias = codebook, correction, bias
+        self.spec = spec
+        self.output_dtype = output_dtype
+
+    @property
+    def in_features(self) -> int:
+        return int(self.qdata.shape[1]) * 2
+
+    @property
+    def out_features(self) -> int:
+        return int(self.qdata.shape[0])
+
+    def __call__(self, value: torch.Tensor) -> torch.Tensor:
+        out_dtype = self.output_dtype or value.dtype
+        return backend.w4a8_int8_linear(value, self.qdata, self.s_rel, self.s_channel, codebook=self.codebook,
+                                        correction=self.correction, bias=self.bias,
+                                        group_size=self.spec.group_size,
+                                        convrot_groupsize=self.spec.convrot_groupsize, out_dtype=out_dtype,
+                                        convrot=True)
+
+
+def load_w4a8_linear(tensors: Mapping[str, torch.Tensor], prefix: str, *, spec: Mapping | None = None,
+                     device: torch.device | str | None = None,
+                     output_dtype: torch.dtype | None = None) -> W4A8Linear:
+    """Build a ``W4A8Linear`` from checkpoint tensors named as H3 stores them
+    (assembly.py:186-228). ``tensors`` is any mapping (a safetensors
+    ``safe_open`` view wrapped in a dict, a state dict); ``spec`` the
+    file-level quantization metadata (the H3 layout when absent)."""
+    required = (f"{prefix}.weight", f"{prefix}.weight_s_rel", f"{prefix}.weight_s_channel")
+    missing = [k for k in required if k not in tensors]
+    if missing:
+        raise KeyError(f"quantized layer {prefix!r} is not W4A8: missing {missing}")
+    qspec = W4A8QuantSpec.from_mapping(spec) if spec is not None else W4A8QuantSpec()
+
+    def get(key):
+        t = tensors.get(f"{prefix}.{key}")
+        return None if t is None else (t.to(device) if device is not None else t)
+
+    return W4A8Linear(get("weight"), get("weight_s_rel"), get("weight_s_channel"), codebook=get("weight_codebook"),
+                      correction=get("weight_correction"), bias=get("bias"), spec=qspec,
+                      output_dtype=output_dtype)
