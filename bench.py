@@ -4,7 +4,7 @@ Workloads (synthetic, seeded; inputs resident in HBM when the timed region
 starts):
   * W8A8 MLP at the 720p shape: M=25200 tokens, 5120 -> 13824 -> 5120,
     y = fc2(gelu_tanh(fc1(x))) with per-token int8 activations -- `value`
-    (whole-job int8 TOPS, 4*M*d*ffn ops per step, quant/GELU/requant time
+    (whole-job int8 TOPS, 4*M*d*ffn ops per step, quantizer and GELU time
     included);
   * fused AdaLN-RMSNorm + 3D RoPE of Q and K at M=25200, d=5120 (40 x 128),
     reported as HBM GB/s on 8*M*d algorithmic bytes;
@@ -17,8 +17,8 @@ starts):
     against the same kernels with a separate addcmul_.
 
 A step is one pass of the MLP block over the batch. The timed region runs the
-four MLP kernels (per-token quant, fc1 GEMM + dequant/GELU/row-amax epilogue,
-requant, fc2 GEMM + dequant) through the C ABI on torch's current stream, with
+four MLP kernels (per-token quant, fc1 GEMM + dequant epilogue, GELU + per-token
+quant, fc2 GEMM + dequant) through the C ABI on torch's current stream, with
 HIP events between them on that stream, so per-kernel durations come from the
 same region. The CPU baseline is the oracle (torch-CPU restatement of the
 reference's eager path) on a bounded row sample, run on this host's cores.
@@ -48,7 +48,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 # 0.5 GiB by FETCH_SIZE and 1 GiB by WRITE_SIZE, so FETCH_SIZE is scaled x2 and
 # WRITE_SIZE x1 (see profiles/).
 TRAFFIC_BYTES = {
-    "fc1_gemm_gelu": (1499110.6 * 2 + 701725.0) * 1024,
+    "fc1_gemm": (1499110.6 * 2 + 701725.0) * 1024,
     "fc2_gemm": (1478203.0 * 2 + 255960.0) * 1024,
     "norm_rope": (265143.7 * 2 + 504016.5) * 1024,
 }
@@ -288,7 +288,6 @@ def main() -> int:
     q1 = torch.empty(M, D, dtype=torch.int8, device=dev)
     sx = torch.empty(M, dtype=torch.float32, device=dev)
     g = torch.empty(M, F, dtype=torch.bfloat16, device=dev)
-    amax = torch.empty(M, dtype=torch.int32, device=dev)
     q2 = torch.empty(M, F, dtype=torch.int8, device=dev)
     sg = torch.empty(M, dtype=torch.float32, device=dev)
     y = torch.empty(M, D, dtype=torch.bfloat16, device=dev)
@@ -297,16 +296,14 @@ def main() -> int:
     def step(ev):
         if ev:
             ev[0].record()
-        _lib.call("xmh3_quantize_int8_rowwise_ex", x.data_ptr(), 2, 0, M, D, D, q1.data_ptr(), sx.data_ptr(),
-                  amax.data_ptr(), st)
+        _lib.call("xmh3_quantize_int8_rowwise", x.data_ptr(), 2, 0, M, D, D, q1.data_ptr(), sx.data_ptr(), st)
         if ev:
             ev[1].record()
         _lib.call("xmh3_int8_gemm", q1.data_ptr(), D, w1.data_ptr(), D, M, F, D, sx.data_ptr(), s1.data_ptr(), 1,
-                  None, g.data_ptr(), 2, F, 1, amax.data_ptr(), st)
+                  None, g.data_ptr(), 2, F, 0, None, st)
         if ev:
             ev[2].record()
-        _lib.call("xmh3_requant_int8_rows", g.data_ptr(), 2, M, F, F, amax.data_ptr(), q2.data_ptr(),
-                  sg.data_ptr(), st)
+        _lib.call("xmh3_quantize_int8_rowwise", g.data_ptr(), 2, 1, M, F, F, q2.data_ptr(), sg.data_ptr(), st)
         if ev:
             ev[3].record()
         _lib.call("xmh3_int8_gemm", q2.data_ptr(), F, w2.data_ptr(), F, M, D, F, sg.data_ptr(), s2.data_ptr(), 1,
@@ -322,13 +319,13 @@ def main() -> int:
         step(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    names = ("quant", "fc1_gemm_gelu", "requant", "fc2_gemm")
+    names = ("quant", "fc1_gemm", "gelu_quant", "fc2_gemm")
     kavg = {n: statistics.mean(ev[j].elapsed_time(ev[j + 1]) for ev in evs) for j, n in enumerate(names)}
     ms_step = wall * 1e3 / args.steps
     ops = 4.0 * M * D * F
     tops = ops / (ms_step * 1e-3) / 1e12
     gemm_ops = 2.0 * M * D * F
-    fc1_tops = gemm_ops / (kavg["fc1_gemm_gelu"] * 1e-3) / 1e12
+    fc1_tops = gemm_ops / (kavg["fc1_gemm"] * 1e-3) / 1e12
     fc2_tops = gemm_ops / (kavg["fc2_gemm"] * 1e-3) / 1e12
     log(f"mlp: {ms_step:.3f} ms/step wall ({tops:.1f} TOPS), kernel sum {sum(kavg.values()):.3f} ms: "
         + ", ".join(f"{k}={v:.3f}" for k, v in kavg.items()))
@@ -402,10 +399,10 @@ def main() -> int:
                    "norm_rope_workload": "norm_rope_720p", "grid": [7, 45, 80], "heads": 40, "head_dim": 128},
         "frac_of_peak": round(tops / PEAK_INT8_TOPS, 4),
         "kernels_ms": {k: round(v, 4) for k, v in kavg.items()},
-        "roofline": {"kernel": "gemm_i8_v5_kernel (fc1, dequant+GELU+row-amax epilogue)", "bound": "mfma",
+        "roofline": {"kernel": "gemm_i8_v5_kernel (fc1, dequant epilogue)", "bound": "mfma",
                      "achieved": round(fc1_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(fc1_tops / PEAK_INT8_TOPS, 4),
-                     "traffic": round(TRAFFIC_BYTES["fc1_gemm_gelu"]),
+                     "traffic": round(TRAFFIC_BYTES["fc1_gemm"]),
                      "algorithmic": "2*M*d*ffn int8 ops per launch (unit: 1e12 int8 ops/s)"},
         "roofline_fc2": {"kernel": "gemm_i8_v5_kernel (fc2, dequant epilogue)", "bound": "mfma",
                          "achieved": round(fc2_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",

@@ -188,8 +188,9 @@ def test_int8_linear_gelu_input_act(pkg, dev):
 # --------------------------------------------------------------------------- MLP
 
 def _mlp_stages(pkg, dev, inp):
-    """Run the four MLP kernels one by one through the C ABI and return every
-    intermediate (the fused op runs the same launches)."""
+    """The MLP as the GELU-epilogue chain (fc1 epilogue 1 with the row |max|,
+    then the requant entry point), one kernel at a time through the C ABI,
+    returning every intermediate."""
     from x_minimaxh3_amd import _lib
 
     x = inp["x"].to(dev)
@@ -242,6 +243,48 @@ def test_mlp_small_stagewise(pkg, dev):
     q2_mism = (st["q2"] != p["q2"]).float().mean().item()
     say(f"  requant code mismatch vs oracle end-to-end: {q2_mism:.2e}")
     close(st["y"], yr, "mlp output")
+
+
+def test_mlp_small_quantizer_gelu_chain(pkg, dev):
+    """The chain xmh3_w8a8_mlp runs: quant -> fc1 with the dequant epilogue
+    (h) -> per-token quant with the GELU input act -> fc2; every stage against
+    the oracle, and the fused entry point equal to the stages bit for bit."""
+    say("w8a8 mlp 1024x1536x6144: quantizer-GELU chain stagewise")
+    from x_minimaxh3_amd import _lib
+
+    from x_minimaxh3_amd import workloads
+
+    inp = workloads.mlp_inputs(**workloads.CONFIGS["mlp_small"], seed=0)
+    yr, p = cpu_ref.w8a8_mlp(inp["x"], inp["w1"], inp["s1"], inp["w2"], inp["s2"], return_parts=True)
+    x = inp["x"].to(dev)
+    w1, s1, w2, s2 = (inp[k].to(dev) for k in ("w1", "s1", "w2", "s2"))
+    m, d = x.shape
+    f = w1.shape[0]
+    st = _lib.stream_of(x)
+    q1 = torch.empty(m, d, dtype=torch.int8, device=dev)
+    sx = torch.empty(m, dtype=torch.float32, device=dev)
+    h = torch.empty(m, f, dtype=torch.bfloat16, device=dev)
+    q2 = torch.empty(m, f, dtype=torch.int8, device=dev)
+    sg = torch.empty(m, dtype=torch.float32, device=dev)
+    y = torch.empty(m, d, dtype=torch.bfloat16, device=dev)
+    _lib.call("xmh3_quantize_int8_rowwise", x.data_ptr(), 2, 0, m, d, d, q1.data_ptr(), sx.data_ptr(), st)
+    _lib.call("xmh3_int8_gemm", q1.data_ptr(), d, w1.data_ptr(), d, m, f, d, sx.data_ptr(), s1.data_ptr(), 1,
+              None, h.data_ptr(), 2, f, 0, None, st)
+    _lib.call("xmh3_quantize_int8_rowwise", h.data_ptr(), 2, 1, m, f, f, q2.data_ptr(), sg.data_ptr(), st)
+    _lib.call("xmh3_int8_gemm", q2.data_ptr(), f, w2.data_ptr(), f, m, d, f, sg.data_ptr(), s2.data_ptr(), 1,
+              None, y.data_ptr(), 2, d, 0, None, st)
+    yf = pkg.w8a8_mlp(x, w1, s1, w2, s2)
+    torch.cuda.synchronize()
+    assert same(q1, p["q1"], "q1") and same(h, p["h"], "h")
+    g_ref = cpu_ref.gelu_tanh(p["h"])
+    q2r, s2r = cpu_ref.quantize_int8_rowwise(g_ref)
+    mism, dq = _code_stats(q2, q2r, "gelu quant codes")
+    assert mism < 1e-3 and dq <= 1
+    assert torch.allclose(sg.cpu(), s2r.reshape(-1), rtol=2 ** -7, atol=0)
+    yr2 = cpu_ref.dequant(cpu_ref.int8_mm(q2.cpu(), inp["w2"]), sg.cpu(), inp["s2"])
+    assert same(y, yr2, "fc2 given the GPU's q2")
+    assert same(yf, y.cpu(), "fused entry point vs stages")
+    close(y, yr, "mlp output")
 
 
 def test_mlp_fused_op_small(pkg, dev):

@@ -114,15 +114,15 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 // GELU with the tanh approximation, 0.5*h*(1+tanh(u)),
 // u = sqrt(2/pi)*(h + 0.044715*h^3), evaluated as h / (1 + exp(-2u)) (the
-// same function; no cancellation as tanh(u) -> -1). Constants from the
-// published formula.
+// same function; no cancellation as tanh(u) -> -1). The exponent
+// -2u*log2(e) is h * (c1 + c2*h^2) with c1 = -2*log2(e)*sqrt(2/pi) and
+// c2 = 0.044715*c1 (constants from the published formula, products formed in
+// double): three VALU operations before the exp.
 __device__ __forceinline__ float gelu_tanh_f32(float h) {
-  const float kBeta = 0.7978845608028654f;   // sqrt(2/pi)
-  const float kKappa = 0.044715f;
-  float cube = h * h * h;
-  float u = kBeta * (h + kKappa * cube);
-  // exp(-2u) = 2^(-2u*log2(e))
-  float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);
+  const float c1 = -2.3022082f;    // -2 * log2(e) * sqrt(2/pi)
+  const float c2 = -0.10294324f;   // 0.044715 * c1
+  const float a = h * __builtin_fmaf(c2, h * h, c1);
+  const float e = __builtin_amdgcn_exp2f(a);
   return h * __builtin_amdgcn_rcpf(1.0f + e);
 }
 

@@ -86,6 +86,28 @@ __device__ __forceinline__ int quant_code_rcp(float x, float sT, float inv) {
   }
 }
 
+// Four codes packed into one word (byte j = code of x_j). The clamp comes
+// before the rounding to an integer (the bounds are integers, so the order
+// does not change the result), and c + 1.5 * 2^23 rounds c to the nearest
+// even integer in the low bits of its fp32 pattern: its low byte is the
+// two's-complement code. Bytes are gathered with v_perm.
+template <typename T>
+__device__ __forceinline__ float quant_value(float x, float sT, float inv) {
+  if constexpr (std::is_same<T, BF16T>::value) return T::round(x * inv);   // see quant_code_rcp
+  else return T::round(x / sT);
+}
+template <typename T>
+__device__ __forceinline__ uint32_t quant_word4(float x0, float x1, float x2, float x3, float sT, float inv) {
+  const float m = 12582912.0f;   // 1.5 * 2^23
+  const uint32_t y0 = __float_as_uint(__builtin_amdgcn_fmed3f(quant_value<T>(x0, sT, inv), -128.0f, 127.0f) + m);
+  const uint32_t y1 = __float_as_uint(__builtin_amdgcn_fmed3f(quant_value<T>(x1, sT, inv), -128.0f, 127.0f) + m);
+  const uint32_t y2 = __float_as_uint(__builtin_amdgcn_fmed3f(quant_value<T>(x2, sT, inv), -128.0f, 127.0f) + m);
+  const uint32_t y3 = __float_as_uint(__builtin_amdgcn_fmed3f(quant_value<T>(x3, sT, inv), -128.0f, 127.0f) + m);
+  const uint32_t lo = __builtin_amdgcn_perm(y1, y0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(y3, y2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 template <typename T>
 __device__ __forceinline__ float scale_for_math(float scale) {
   float sT = T::round(scale);
@@ -116,18 +138,29 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(
     const int64_t col = ((int64_t)i * 64 + lane) * 8;
     if (col < K) {
       load8<T>(xr + col, buf[i]);
+      if constexpr (ACT == ACT_GELU_TANH && sizeof(typename T::storage) == 2) {
+        // T(gelu) of a pair packed by one conversion; |max| of the unrounded
+        // values, rounded once below (rounding is monotone)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float f = get8<T>(buf[i], j);
-        if constexpr (ACT == ACT_GELU_TANH) {
-          f = T::round(gelu_tanh_f32(f));
-          set8<T>(buf[i], j, f);
+        for (int j = 0; j < 8; j += 2) {
+          const float g0 = gelu_tanh_f32(get8<T>(buf[i], j)), g1 = gelu_tanh_f32(get8<T>(buf[i], j + 1));
+          amax = fmaxf(amax, fmaxf(fabsf(g0), fabsf(g1)));
+          (&buf[i].v.x)[j >> 1] = T::store2(g0, g1);
         }
-        amax = fmaxf(amax, fabsf(f));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float f = get8<T>(buf[i], j);
+          if constexpr (ACT == ACT_GELU_TANH) {
+            f = T::round(gelu_tanh_f32(f));
+            set8<T>(buf[i], j, f);
+          }
+          amax = fmaxf(amax, fabsf(f));
+        }
       }
     }
   }
-  amax = wave_max(amax);
+  amax = T::round(wave_max(amax));
   const float s = row_scale(amax);
   const float sT = scale_for_math<T>(s);
   const float inv = 1.0f / sT;
@@ -136,12 +169,9 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(
   for (int i = 0; i < NL; ++i) {
     const int64_t col = ((int64_t)i * 64 + lane) * 8;
     if (col < K) {
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_rcp<T>(get8<T>(buf[i], j), sT, inv) & 0xff) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        hi |= (uint32_t)(quant_code_rcp<T>(get8<T>(buf[i], j + 4), sT, inv) & 0xff) << (8 * j);
+      const Pack8<T>& b = buf[i];
+      const uint32_t lo = quant_word4<T>(get8<T>(b, 0), get8<T>(b, 1), get8<T>(b, 2), get8<T>(b, 3), sT, inv);
+      const uint32_t hi = quant_word4<T>(get8<T>(b, 4), get8<T>(b, 5), get8<T>(b, 6), get8<T>(b, 7), sT, inv);
       *reinterpret_cast<uint2*>(qr + col) = make_uint2(lo, hi);
     }
   }
@@ -219,12 +249,9 @@ __global__ __launch_bounds__(256) void requant_rows_kernel(
 #pragma unroll
     for (int u = 0; u < UNR; ++u) {
       const int c = c0 + u * 64 + lane;
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= (uint32_t)(quant_code_rcp<T>(get8<T>(b[u], j), sT, inv) & 0xff) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        hi |= (uint32_t)(quant_code_rcp<T>(get8<T>(b[u], j + 4), sT, inv) & 0xff) << (8 * j);
+      const Pack8<T>& bb = b[u];
+      const uint32_t lo = quant_word4<T>(get8<T>(bb, 0), get8<T>(bb, 1), get8<T>(bb, 2), get8<T>(bb, 3), sT, inv);
+      const uint32_t hi = quant_word4<T>(get8<T>(bb, 4), get8<T>(bb, 5), get8<T>(bb, 6), get8<T>(bb, 7), sT, inv);
       if (c < chunks) *reinterpret_cast<uint2*>(qr + (int64_t)c * 8) = make_uint2(lo, hi);
     }
   }
