@@ -12,6 +12,8 @@ starts):
   * the long 16x68x120 grid (M=130560): norm-rope + W8A8 MLP in 16384-token
     chunks, HBM-resident (compute rate) and streamed from pinned host memory
     through double-buffered device slots (end-to-end, PCIe included);
+  * H3's two norm call sites at d=5376 (segmented rms_adaln, per-head QK
+    rms_rope with the 96-wide rotation);
   * the SwiGLU + ConvRot-256 row quantizer on H3's fc2 input (25200 x 14336)
     and H3's fc2 with the gated residual update in the GEMM epilogue (d=5376),
     against the same kernels with a separate addcmul_.
@@ -192,6 +194,44 @@ def bench_h3_fc2(pkg, dev, steps: int, warmup: int) -> dict:
                     "unfused = same kernels with a bf16 projection and torch addcmul_"}
 
 
+def bench_h3_norm_modes(pkg, dev, steps: int, warmup: int) -> dict:
+    """The two H3 norm call sites at the 720p token count with H3's width
+    (d=5376 = 56 heads x 96): segmented rms_adaln (norm weight, 3 modulation
+    rows, eps 1e-5; 4*M*d bytes) and the in-place per-head QK rms_rope with the
+    full 96-wide rotation (8*M*d bytes for Q and K)."""
+    import torch
+
+    from x_minimaxh3_amd import h3
+
+    m, heads, hd = 25200, 56, 96
+    d = heads * hd
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(m, d, device=dev, generator=g).bfloat16()
+    w = (1.0 + 0.1 * torch.randn(d, device=dev, generator=g)).bfloat16()
+    scale = (0.1 * torch.randn(3, d, device=dev, generator=g)).bfloat16()
+    shift = (0.1 * torch.randn(3, d, device=dev, generator=g)).bfloat16()
+    segments = ((0, 512, 0), (512, 1024, 1), (1024, m, 2))
+    ms_a = timed(lambda: h3.rms_adaln(x, w, shift, scale, segments, eps=1e-5), steps, warmup)
+    q = torch.randn(m, heads, hd, device=dev, generator=g).bfloat16()
+    k = torch.randn(m, heads, hd, device=dev, generator=g).bfloat16()
+    ang = torch.rand(m, hd // 2, device=dev, generator=g) * 6.283
+    c, sn = torch.cos(ang), torch.sin(ang)
+    freqs = torch.stack((torch.stack((c, -sn), -1), torch.stack((sn, c), -1)), -2).reshape(1, m, 1, hd // 2, 2, 2)
+    qw = (1.0 + 0.1 * torch.randn(hd, device=dev, generator=g)).bfloat16()
+    kw = (1.0 + 0.1 * torch.randn(hd, device=dev, generator=g)).bfloat16()
+    ms_r = timed(lambda: h3.apply_qknorm_rope(q, k, q_weight=qw, k_weight=kw, frequencies=freqs, eps=1e-5),
+                 steps, warmup)
+    gbs_a = 4.0 * m * d / (ms_a * 1e-3) / 1e9
+    gbs_r = 8.0 * m * d / (ms_r * 1e-3) / 1e9
+    return {"workload": "h3_norm_modes_720p", "tokens": m, "d_model": d, "heads": heads, "head_dim": hd,
+            "rms_adaln_us": round(ms_a * 1e3, 2), "rms_adaln_gbs": round(gbs_a, 1),
+            "rms_adaln_frac": round(gbs_a / PEAK_HBM_GBS, 4),
+            "qk_rms_rope_us": round(ms_r * 1e3, 2), "qk_rms_rope_gbs": round(gbs_r, 1),
+            "qk_rms_rope_frac": round(gbs_r / PEAK_HBM_GBS, 4),
+            "note": "rms_adaln: 3 segments, norm weight, eps 1e-5, 4*M*d bytes; QK rms_rope in place on "
+                    "[M, 56, 96] with fp32 table, 8*M*d bytes"}
+
+
 def bench_long(pkg, dev, inp: dict, warmup: int) -> dict:
     import torch
 
@@ -357,12 +397,15 @@ def main() -> int:
     log(f"norm_rope: {nr_ms * 1e3:.1f} us/launch, {nr_gbs:.0f} GB/s ({nr_gbs / PEAK_HBM_GBS:.1%} of 8 TB/s)")
 
     # ------------------------------------------------------------------ W4A8 and long sequence
-    w4 = long = cr = h3fc2 = None
+    w4 = long = cr = h3fc2 = h3norm = None
     if not args.no_extra:
         w4 = bench_w4a8(pkg, dev, max(3, args.steps // 4), 2)
         log(f"w4a8 mlp: {w4['ms_per_step']:.3f} ms/step ({w4['value']} TOPS)")
         cr = bench_convrot(pkg, dev, args.steps, args.warmup)
         log(f"convrot swiglu quant: {cr['us_per_launch']:.1f} us/launch, {cr['achieved']:.0f} GB/s")
+        h3norm = bench_h3_norm_modes(pkg, dev, args.steps, args.warmup)
+        log(f"h3 norm modes: rms_adaln {h3norm['rms_adaln_us']:.1f} us ({h3norm['rms_adaln_gbs']:.0f} GB/s), "
+            f"qk rms_rope {h3norm['qk_rms_rope_us']:.1f} us ({h3norm['qk_rms_rope_gbs']:.0f} GB/s)")
         h3fc2 = bench_h3_fc2(pkg, dev, max(3, args.steps // 2), 2)
         log(f"h3 fc2 gated: fused {h3fc2['ms_fused']:.3f} ms ({h3fc2['value']} TOPS), "
             f"unfused {h3fc2['ms_unfused']:.3f} ms")
@@ -415,6 +458,7 @@ def main() -> int:
         "w4a8_mlp": w4,
         "convrot_quant": cr,
         "h3_fc2_gated": h3fc2,
+        "h3_norm_modes": h3norm,
         "long": long,
         "cpu_baseline": cpu,
         "cpu_baseline_norm_rope": cpu_nr,

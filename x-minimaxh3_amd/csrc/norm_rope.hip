@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
   if (row >= a.rows) return;
   const int64_t items = a.D / EPI;
   const int nt = a.x1 ? 2 : 1;
-  S* lrow = reinterpret_cast<S*>(dyn_lds) + (int64_t)wave * 2 * a.D;
+  S* lrow = reinterpret_cast<S*>(dyn_lds) + (int64_t)wave * nt * a.D;
 
   auto item_off = [&](int64_t u, int64_t& o0, int64_t& o1) {
     if constexpr (ROPE) {
@@ -275,8 +275,33 @@ __global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
   const int64_t trow = a.freqs_row_stride ? row * a.freqs_row_stride : 0;
   bool tab_loaded = false;
 
+  // weight / scale / shift of the items of step s, loaded one step ahead: the
+  // compiler may not move a load above the previous step's stores (the output
+  // could alias them), so the prefetch is explicit
+  constexpr int NH = ROPE ? 2 : 1;
+  struct Mod { V8<TX> w[NH]; V8<TM> sc[NH], sh[NH]; };
+  auto fetch_mod = [&](int s, Mod& m) __attribute__((always_inline)) {
+    const int64_t u = (int64_t)s * 64 + lane;
+    if (u >= items) return;
+    int64_t o0, o1;
+    item_off(u, o0, o1);
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const int64_t col = h ? o1 : o0;
+      if constexpr (WEIGHT) ld8<TX>(a.weight, col, m.w[h]);
+      if constexpr (ADALN) {
+        ld8<TM>(a.scale, mrow * a.mod_ld + col, m.sc[h]);
+        ld8<TM>(a.shift, mrow * a.mod_ld + col, m.sh[h]);
+      }
+    }
+  };
+  Mod mod[2];
+  fetch_mod(0, mod[0]);
+
 #pragma unroll
   for (int s = 0; s < NSTEP; ++s) {
+    if (s + 1 < NSTEP) fetch_mod(s + 1, mod[(s + 1) & 1]);
+    const Mod& m = mod[s & 1];
     const int64_t u = (int64_t)s * 64 + lane;
     if (u >= items) continue;
     int64_t o0, o1;
@@ -287,28 +312,22 @@ __global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
         tab_loaded = true;
       }
     }
-    float y[2][ROPE ? 2 : 1][8];
+    float y[2][NH][8];
 #pragma unroll
-    for (int h = 0; h < (ROPE ? 2 : 1); ++h) {
-      const int64_t col = h ? o1 : o0;
+    for (int h = 0; h < NH; ++h) {
       float w8[8], t8[8], sh8[8];
       if constexpr (WEIGHT) {
-        V8<TX> wv;
-        ld8<TX>(a.weight, col, wv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) w8[j] = g8<TX>(wv, j);
+        for (int j = 0; j < 8; ++j) w8[j] = g8<TX>(m.w[h], j);
       }
       if constexpr (ADALN) {
-        V8<TM> sv, hv;
-        ld8<TM>(a.scale, mrow * a.mod_ld + col, sv);
-        ld8<TM>(a.shift, mrow * a.mod_ld + col, hv);
 #pragma unroll
         for (int j = 0; j < 8; j += 2) {
-          t8[j] = 1.0f + g8<TM>(sv, j);          // (1 + scale) in scale's dtype
-          t8[j + 1] = 1.0f + g8<TM>(sv, j + 1);
+          t8[j] = 1.0f + g8<TM>(m.sc[h], j);          // (1 + scale) in scale's dtype
+          t8[j + 1] = 1.0f + g8<TM>(m.sc[h], j + 1);
           TM::round2(t8[j], t8[j + 1]);
-          sh8[j] = g8<TM>(hv, j);
-          sh8[j + 1] = g8<TM>(hv, j + 1);
+          sh8[j] = g8<TM>(m.sh[h], j);
+          sh8[j + 1] = g8<TM>(m.sh[h], j + 1);
         }
       }
 #pragma unroll
@@ -628,6 +647,17 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     ld8<TX>(a.x, xoff + c0, v0);
     if (is_pair) ld8<TX>(a.x, xoff + c1, v1);
   }
+  // the norm weight and the table do not depend on the reduction: their loads
+  // go out with the row's, so the element pass waits on one memory latency
+  V8<TW> wv0, wv1;
+  Tab8<TF> tab;
+  if constexpr (NORM) {
+    if (is_pair || is_tail) {
+      ld8<TW>(a.weight, c0, wv0);
+      if (is_pair) ld8<TW>(a.weight, c1, wv1);
+    }
+  }
+  if (is_pair) load_tab8<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 8 * 4, tab);
   float rr = 1.0f;
   if constexpr (NORM) {
     // per-head sum of squares in the reference's order (see ref_order_sumsq):
@@ -663,34 +693,46 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     }
     const int gbase = lane - (lane % LPH);
     float fin = 0.0f;
+    if constexpr (LPH <= 8) {
+      // chain L = v + 8r sits on lane v % LPH, slot L / LPH: the 4-row sum of
+      // lane-vector v is local to one lane; only the 8 row sums travel
+      constexpr int NV = 8 / LPH;
+      float rs[NV];
 #pragma unroll
-    for (int v = 0; v < 8; ++v) {
-      float rsum = 0.0f;
+      for (int k = 0; k < NV; ++k) {
+        float r = tch[k];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int L = v + 8 * r;
-        const float t = __shfl(tch[(L / LPH) < NCH ? (L / LPH) : 0], gbase + (L % LPH), 64);
-        rsum = r ? rsum + t : t;
+        for (int q = 1; q < 4; ++q) r = r + tch[k + q * NV];
+        rs[k] = r;     // lane-vector v = it + k * LPH
       }
-      fin = fin + rsum;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) fin = fin + __shfl(rs[v / LPH], gbase + (v % LPH), 64);
+    } else {
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        float rsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int L = v + 8 * r;
+          const float t = __shfl(tch[(L / LPH) < NCH ? (L / LPH) : 0], gbase + (L % LPH), 64);
+          rsum = r ? rsum + t : t;
+        }
+        fin = fin + rsum;
+      }
     }
     rr = 1.0f / sqrtf(fin / (float)a.D + a.eps);
   }
   if (!live || !(is_pair || is_tail)) return;
 
-  auto normalise = [&](V8<TX>& vv, int64_t col) {
+  auto normalise = [&](V8<TX>& vv, const V8<TW>& wv) {
     if constexpr (NORM) {
-      V8<TW> wv;
-      ld8<TW>(a.weight, col, wv);
 #pragma unroll
       for (int j = 0; j < 8; ++j) s8<TX>(vv, j, TX::round((g8<TX>(vv, j) * rr) * g8<TW>(wv, j)));
     }
   };
-  normalise(v0, c0);
+  normalise(v0, wv0);
   if (is_pair) {
-    normalise(v1, c1);
-    Tab8<TF> tab;
-    load_tab8<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 8 * 4, tab);
+    normalise(v1, wv1);
     V8<TX> r0, r1;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -712,8 +754,11 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
 // ---------------------------------------------------------------------------
 template <typename TX, typename TM, typename TF, bool ROPE, bool ADALN, bool WEIGHT, int IPH, int N>
 static int launch_row_n(RowArgs& a, hipStream_t st) {
-  const size_t per_wave = 2 * (size_t)a.D * sizeof(typename TX::storage);
-  const int wpb = (int)std::min<size_t>(4, (160 * 1024) / per_wave);
+  // one LDS row per tensor per wave; two waves per workgroup, so that several
+  // workgroups share a CU's LDS (one wave per row and nothing else in flight:
+  // the occupancy is what hides the memory latency)
+  const size_t per_wave = (a.x1 ? 2 : 1) * (size_t)a.D * sizeof(typename TX::storage);
+  const int wpb = (int)std::min<size_t>(2, (160 * 1024) / per_wave);
   if (a.D % 8 != 0 || a.D >= (1 << 17) || wpb < 1)
     return fail(XMH3_EUNSUPPORTED, "row-span kernel: width must be a multiple of 8 and below 2^17");
   auto kern = rowspan_exact_kernel<TX, TM, TF, ROPE, ADALN, WEIGHT, IPH, N>;
