@@ -679,26 +679,42 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_v5_kernel(GemmArgs p) {
   // its first read; B (slice t+1 has landed in every wave) at sub-step 1.
   // DMA pairs 0-5 go out in sub-step 0 after barrier A, pairs 6-7 in sub-step
   // 1, so vmcnt <= 12 at B means slice t+1 is complete.
+#ifndef XMH3_V5_AROWS
+#define XMH3_V5_AROWS 3
+#endif
+#ifndef XMH3_V5_XEARLY
+#define XMH3_V5_XEARLY 0
+#endif
+  // AROWS MFMA rows on X run before barrier A (time for the Y reads to land);
+  // the remaining rows carry the first 8 - AROWS DMA pairs of slice t+2
+  constexpr int AROWS = XMH3_V5_AROWS, PRE = 8 - AROWS;
   auto step = [&](int t, auto STG) __attribute__((always_inline)) {
     constexpr int s = decltype(STG)::value;
     const int knext = min(t + 2, ksteps - 1);
     wait_lgkm0();                       // X = (t, k0) in registers
     load_frags(STG, C1{}, ya, yb);      // Y = (t, k1): the last reads of stage s
-    mfma_row(C0{}, xa, xb);
-    mfma_row(C1{}, xa, xb);
+    static_for<AROWS>([&](auto I) { mfma_row(I, xa, xb); });
     __builtin_amdgcn_sched_barrier(0);
     wait_lgkm0();
     asm volatile("s_barrier" ::: "memory");   // A
-    static_for<6>([&](auto G) {
+    static_for<PRE>([&](auto G) {
       issue_pair(G, knext, STG);
-      mfma_row(std::integral_constant<int, G + 2>{}, xa, xb);
+      mfma_row(std::integral_constant<int, G + AROWS>{}, xa, xb);
       __builtin_amdgcn_sched_barrier(0);
     });
-    wait_vmcnt<12>();
+    wait_vmcnt<2 * PRE>();
     asm volatile("s_barrier" ::: "memory");   // B
     static_for<8>([&](auto G) {
-      if constexpr (G >= 6) issue_pair(G, knext, STG);
+      if constexpr (G >= PRE) issue_pair(G, knext, STG);
+#if XMH3_V5_XEARLY
+      // next step's X fragments two pairs per row over the first half
+      if constexpr (G < 4) {
+        load_pair(std::integral_constant<int, s ^ 1>{}, C0{}, 2 * G, xa, xb);
+        load_pair(std::integral_constant<int, s ^ 1>{}, C0{}, 2 * G + 1, xa, xb);
+      }
+#else
       load_pair(std::integral_constant<int, s ^ 1>{}, C0{}, G, xa, xb);
+#endif
       mfma_row(G, ya, yb);
       __builtin_amdgcn_sched_barrier(0);
     });
