@@ -68,3 +68,39 @@ def test_argument_errors_need_no_gpu(pkg):
     assert rc == 1 and b"input_act" in lib.xmh3_last_error()
     rc = lib.xmh3_w8a8_mlp(None, 2, 8, 100, 64, 100, None, None, 1, None, None, 1, None, 100, None, 0, None)
     assert rc == 1 and b"multiples of 16" in lib.xmh3_last_error()
+
+
+def test_argument_errors_of_the_h3_entry_points(pkg):
+    """The ConvRot quantizer, the gated-residual GEMM and the W4A8 group sums
+    reject bad shapes before any launch (the pointers below are never
+    dereferenced: every case fails validation first)."""
+    from x_minimaxh3_amd import _lib
+
+    lib = _lib.load()
+    fake = 4096   # aligned, never used
+    err = lambda: lib.xmh3_last_error()
+    # ConvRot quantizer: group, width, activation
+    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 256, 256, 64, fake, fake, None) == 1
+    assert b"convrot_groupsize" in err()
+    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 100, 128, 256, fake, fake, None) == 1
+    assert b"multiple of 256" in err()
+    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 16640, 16640, 256, fake, fake, None) == 1
+    assert b"16384" in err()
+    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 5, 4, 256, 256, 256, fake, fake, None) == 1
+    assert b"activation" in err()
+    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 1, 4, 256, 256, 0, fake, fake, None) == 3
+    assert b"only swiglu" in err()
+    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 0, 0, 4, 256, 256, 256, fake, fake, None) == 3
+    assert b"bf16 or fp16" in err()
+    # gated residual: width multiple of 4, residual dtype, gate dtype, gate rows
+    args = lambda n, rdt, gdt, nrows: (fake, 512, fake, 512, 8, n, 512, fake, fake, 1, None, fake, rdt, n + 2,
+                                       fake, gdt, n + 2, nrows, fake, None)
+    assert lib.xmh3_int8_gemm_gated_residual(*args(6, 2, 0, 1)) == 1 and b"multiples of 4" in err()
+    assert lib.xmh3_int8_gemm_gated_residual(*args(8, 0, 0, 1)) == 1 and b"bf16 or fp16" in err()
+    assert lib.xmh3_int8_gemm_gated_residual(*args(8, 2, 1, 1)) == 1 and b"gate must be" in err()
+    assert lib.xmh3_int8_gemm_gated_residual(*args(8, 2, 0, 0)) == 1 and b"gate table" in err()
+    # W4A8 correction group sums
+    assert lib.xmh3_int8_group_sums(fake, 64, fake, 4, 60, 16, fake, 2, 4, None) == 1
+    assert b"multiple of group_size" in err()
+    assert lib.xmh3_int8_group_sums(fake, 64, fake, 4, 64, 16, fake, 7, 4, None) == 3
+    assert b"out dtype" in err()
