@@ -438,6 +438,29 @@ def test_rope_only_bit_exact(pkg, dev):
     assert torch.equal(q2.cpu(), cpu_ref.apply_rope_split_half1(xq, tab))
 
 
+@pytest.mark.parametrize("heads,per_head_table", [(2, False), (8, True), (56, False)])
+def test_rope_table_paths(pkg, dev, heads, per_head_table):
+    """The head-span kernel stages a token's table row in LDS when every head
+    shares it and a block spans few tokens; per-head tables and few heads per
+    token take the direct loads. Both against the oracle, bit for bit."""
+    say(f"rope table paths heads={heads} per_head_table={per_head_table}")
+    g = torch.Generator().manual_seed(24 + heads)
+    S, D = 45, 96
+    xq = torch.randn(1, S, heads, D, generator=g).to(torch.bfloat16)
+    xk = torch.randn(1, S, heads, D, generator=g).to(torch.bfloat16)
+    th = heads if per_head_table else 1
+    ang = torch.rand(1, S, th, D // 2, generator=g) * 40
+    c, sn = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -sn, sn, c), -1).reshape(1, S, th, D // 2, 2, 2)
+    qw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    q2, k2 = xq.to(dev), xk.to(dev)
+    pkg.rms_rope_split_half_(q2, k2, tab.to(dev), qw.to(dev), kw.to(dev), 1e-5, D)
+    torch.cuda.synchronize()
+    assert same(q2, cpu_ref.rms_rope_split_half1(xq, tab, qw, 1e-5, D), "q")
+    assert same(k2, cpu_ref.rms_rope_split_half1(xk, tab, kw, 1e-5, D), "k")
+
+
 def test_h3_qknorm_rope_partial_inplace(pkg, dev):
     """H3 call form: per-head RMSNorm with weight, eps 1e-5, partial rotary 96
     of 128 with a bf16 table, in place on views of a packed QKV tensor."""

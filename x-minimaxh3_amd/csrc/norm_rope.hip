@@ -620,7 +620,31 @@ struct HeadArgs {
   float eps;
 };
 
-template <typename TX, typename TW, typename TF, bool NORM, int LPH>
+// TABL: the table is shared by the heads of a token (head stride 0) and the
+// block's heads span at most 8 tokens; the block stages those table rows in
+// LDS once instead of every pair lane reading its 128 bytes from L2.
+template <typename TF>
+__device__ __forceinline__ void lds_tab8(const uint8_t* p, Tab8<TF>& t) {
+  V8<TF> raw[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint8_t* pq = p + q * 8 * (int)sizeof(typename TF::storage);
+    if constexpr (sizeof(typename TF::storage) == 4) {
+      raw[q].v[0] = *reinterpret_cast<const uint4*>(pq);
+      raw[q].v[1] = *reinterpret_cast<const uint4*>(pq + 16);
+    } else {
+      raw[q].v = *reinterpret_cast<const uint4*>(pq);
+    }
+  }
+#pragma unroll
+  for (int pp = 0; pp < 8; ++pp)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t.f[pp][e] = g8<TF>(raw[(pp * 4 + e) >> 3], (pp * 4 + e) & 7);
+}
+
+constexpr int HEAD_TAB_ROWS = 8, HEAD_TAB_ROW_BYTES = 1024;   // rot <= 128, fp32
+
+template <typename TX, typename TW, typename TF, bool NORM, int LPH, bool TABL>
 __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t head = (int64_t)blockIdx.x * (256 / LPH) + threadIdx.x / LPH;
@@ -657,7 +681,29 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
       if (is_pair) ld8<TW>(a.weight, c1, wv1);
     }
   }
-  if (is_pair) load_tab8<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 8 * 4, tab);
+  if constexpr (TABL) {
+    __shared__ __attribute__((aligned(16))) uint8_t tabs[HEAD_TAB_ROWS * HEAD_TAB_ROW_BYTES];
+    constexpr int G = 256 / LPH;
+    const int64_t first = (int64_t)blockIdx.x * G;
+    const int64_t last = (first + G < nheads ? first + G : nheads) - 1;
+    const int64_t bs0 = first / a.H;
+    const int nrow = (int)(last / a.H - bs0 + 1);          // <= HEAD_TAB_ROWS (host)
+    const int row_bytes = half * 4 * (int)sizeof(typename TF::storage);
+    const int chunks = row_bytes / 16;
+    for (int i = threadIdx.x; i < nrow * chunks; i += 256) {
+      const int rrow = i / chunks, c = i - rrow * chunks;
+      const int64_t bsr = bs0 + rrow, sr = bsr % a.S, br = bsr / a.S;
+      const uint8_t* src = static_cast<const uint8_t*>(a.freqs) +
+                           (br * a.fb + sr * a.fs) * (int64_t)sizeof(typename TF::storage);
+      *reinterpret_cast<uint4*>(tabs + rrow * HEAD_TAB_ROW_BYTES + c * 16) =
+          *reinterpret_cast<const uint4*>(src + c * 16);
+    }
+    __syncthreads();
+    if (is_pair && live)
+      lds_tab8<TF>(tabs + (bs - bs0) * HEAD_TAB_ROW_BYTES + it * 8 * 4 * (int)sizeof(typename TF::storage), tab);
+  } else {
+    if (is_pair) load_tab8<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 8 * 4, tab);
+  }
   float rr = 1.0f;
   if constexpr (NORM) {
     // per-head sum of squares in the reference's order (see ref_order_sumsq):
@@ -927,13 +973,28 @@ int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D,
 template <typename TX, typename TW, typename TF, bool NORM>
 static int launch_head(HeadArgs& a, int lph, hipStream_t st) {
   const int64_t nheads = a.B * a.S * a.H;
+  // table rows through LDS: shared by the heads of a token, at most
+  // HEAD_TAB_ROWS tokens per block, rows of at most HEAD_TAB_ROW_BYTES
+  auto tabl_ok = [&](int L) {
+    const int64_t g = 256 / L;
+    return a.fh == 0 && (int64_t)(a.rot / 2) * 4 * (int64_t)sizeof(typename TF::storage) <= HEAD_TAB_ROW_BYTES &&
+           (g - 1) / a.H + 2 <= HEAD_TAB_ROWS;
+  };
 #define XMH3_H(L)                                                                               \
   if (lph == L) {                                                                               \
     dim3 grid((unsigned)((nheads + (256 / L) - 1) / (256 / L)));                                \
-    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L>), grid, dim3(256), 0, st, a);      \
+    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L, false>), grid, dim3(256), 0, st, a); \
     return check_launch("headspan_kernel");                                                     \
   }
+#define XMH3_HT(L)                                                                              \
+  if (lph == L && tabl_ok(L)) {                                                                 \
+    dim3 grid((unsigned)((nheads + (256 / L) - 1) / (256 / L)));                                \
+    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L, true>), grid, dim3(256), 0, st, a); \
+    return check_launch("headspan_kernel");                                                     \
+  }
+  XMH3_HT(4) XMH3_HT(8) XMH3_HT(16)
   XMH3_H(1) XMH3_H(2) XMH3_H(4) XMH3_H(8) XMH3_H(16) XMH3_H(32) XMH3_H(64)
+#undef XMH3_HT
 #undef XMH3_H
   return fail(XMH3_EUNSUPPORTED, "head-span kernel: head too wide");
 }
