@@ -188,7 +188,10 @@ __device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool nok = n + r < p.N;
-          float y = TO::round((float)acc[i][j][r] * (sxm * sc.sw[j][r]));
+          float y = (float)acc[i][j][r] * (sxm * sc.sw[j][r]);
+          // the stores round to TO once; the bias add and GELU need the value
+          // in TO first (the reference materialises it there)
+          if constexpr (BIAS || EPI == EPI_GELU) y = TO::round(y);
           if constexpr (BIAS) y = TO::round(y + TO::load(brow[min(n + r, p.N - 1)]));
           if constexpr (EPI == EPI_GELU) {
             y = TO::round(gelu_tanh_f32(y));
