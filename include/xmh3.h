@@ -24,6 +24,9 @@
 
 #include <stddef.h>
 #include <stdint.h>
+#ifndef __cplusplus
+#include <stdbool.h>
+#endif
 
 #ifdef __cplusplus
 extern "C" {
@@ -226,6 +229,30 @@ int xmh3_rope_split_half(void* x, void* out, int dtype, int64_t B, int64_t S, in
                          const void* norm_weight, int weight_dtype, const void* freqs,
                          int freqs_dtype, const int64_t* freqs_strides, int rot_dim, float eps,
                          int norm, xmh3_stream_t stream);
+
+/*
+ * The reference's per-head RMSNorm + RoPE launcher under its own name and
+ * 46-argument list (7 pointers; batch, dim1, dim2, head_dim, rot_dim; the
+ * table's three leading sizes; 4 strides each of q, k, q_out, k_out; 6 table
+ * strides; the q / k weight strides; epsilon; input, table and weight dtype
+ * codes; has_k; split_half; stream), so a ctypes caller with pinned argtypes
+ * (h3serve/native_engine/model/single_qknorm_rope.py:36-66,158-187) binds
+ * this library unchanged. Runs the head-span kernel of xmh3_rope_split_half.
+ * Returns nothing, as the reference does: an argument outside this build's
+ * support (interleaved pairs, a strided head dimension, weight or table pair
+ * layout) launches nothing and sets xmh3_last_error().
+ * Replaces: CK/backends/cuda/ops/rms_rope.cu:353-384 launch_rms_rope_kernel.
+ */
+void launch_rms_rope_kernel(const void* q, const void* k, const void* freqs, const void* q_scale,
+                            const void* k_scale, void* q_out, void* k_out, int64_t batch, int64_t dim1,
+                            int64_t dim2, int64_t head_dim, int64_t rot_dim, int64_t freqs_batch,
+                            int64_t freqs_dim1, int64_t freqs_dim2, int64_t q_s0, int64_t q_s1, int64_t q_s2,
+                            int64_t q_s3, int64_t k_s0, int64_t k_s1, int64_t k_s2, int64_t k_s3,
+                            int64_t qo_s0, int64_t qo_s1, int64_t qo_s2, int64_t qo_s3, int64_t ko_s0,
+                            int64_t ko_s1, int64_t ko_s2, int64_t ko_s3, int64_t f_s0, int64_t f_s1,
+                            int64_t f_s2, int64_t f_s3, int64_t f_s4, int64_t f_s5, int64_t qs_stride,
+                            int64_t ks_stride, float epsilon, int input_dtype_code, int freqs_dtype_code,
+                            int scale_dtype_code, bool has_k, bool split_half, xmh3_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -15,7 +15,7 @@ LIB = ROOT / "x-minimaxh3_amd" / "libxmh3_hip.so"
 def declared_symbols() -> set[str]:
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return set(re.findall(r"\b(xmh3_[a-z0-9_]+)\s*\(", text))
+    return set(re.findall(r"\b((?:xmh3_|launch_)[a-z0-9_]+)\s*\(", text))
 
 
 def test_header_declares_entry_points():
@@ -104,3 +104,29 @@ def test_argument_errors_of_the_h3_entry_points(pkg):
     assert b"multiple of group_size" in err()
     assert lib.xmh3_int8_group_sums(fake, 64, fake, 4, 64, 16, fake, 7, 4, None) == 3
     assert b"out dtype" in err()
+
+
+def test_reference_rope_launcher_signature(pkg):
+    """launch_rms_rope_kernel keeps the reference's 46-argument list (the
+    argtypes single_qknorm_rope.py pins) and rejects what this build does not
+    take without launching anything."""
+    from x_minimaxh3_amd import _lib
+
+    res, args = _lib.SIGNATURES["launch_rms_rope_kernel"]
+    assert res is None and len(args) == 46
+    assert args == [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 32 + [ctypes.c_float] + [ctypes.c_int] * 3 + \
+        [ctypes.c_bool] * 2 + [ctypes.c_void_p]
+    lib = _lib.load()
+    fake = 4096
+    base = [fake, None, fake, fake, None, fake, None, 1, 8, 4, 128, 128, 1, 8, 1,
+            4096, 512, 128, 1, 0, 0, 0, 0, 4096, 512, 128, 1, 0, 0, 0, 0,
+            0, 256, 0, 4, 2, 1, 1, 0, 1e-6, 2, 0, 2, False, True, None]
+    assert len(base) == 46
+    interleaved = list(base)
+    interleaved[44] = False
+    lib.launch_rms_rope_kernel(*interleaved)
+    assert b"split-half" in lib.xmh3_last_error()
+    strided = list(base)
+    strided[18] = 2            # q_s3
+    lib.launch_rms_rope_kernel(*strided)
+    assert b"contiguous" in lib.xmh3_last_error()

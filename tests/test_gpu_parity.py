@@ -814,3 +814,39 @@ def test_w4a8_h3_checkpoint_format(pkg, dev):
                                  tensors["fc.weight_s_channel"], codebook=lut, bias=tensors["fc.bias"],
                                  group_size=gs, out_dtype=torch.bfloat16)
     close(y0, y0r, "w4a8 h3 format, no correction")
+
+
+@pytest.mark.parametrize("hnd_out", [False, True])
+def test_reference_named_rope_launcher(pkg, dev, hnd_out):
+    """launch_rms_rope_kernel called with the reference's 46 arguments the way
+    the H3 single-sided QK-norm binding forms them: value [tokens, heads, D]
+    in place, or into an HND-backed NHD view; rot 96 of 128, bf16 table."""
+    say(f"launch_rms_rope_kernel hnd_out={hnd_out}")
+    import ctypes
+
+    from x_minimaxh3_amd import _lib
+
+    g = torch.Generator().manual_seed(25)
+    T, H, D, rot = 77, 6, 128, 96
+    x = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    ang = torch.rand(1, T, 1, rot // 2, generator=g) * 30
+    c, sn = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -sn, sn, c), -1).reshape(1, T, 1, rot // 2, 2, 2).to(torch.bfloat16)
+    w = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    xd, td, wd = x.to(dev), tab.to(dev), w.to(dev)
+    if hnd_out:
+        backing = torch.zeros(H, T, D, dtype=torch.bfloat16, device=dev)
+        out = backing.transpose(0, 1)                 # logical [T, H, D], strides (D, T*D, 1)
+    else:
+        out = xd
+    q4, o4 = xd.unsqueeze(0), out.unsqueeze(0)
+    z4 = (0, 0, 0, 0)
+    args = ([q4.data_ptr(), None, td.data_ptr(), wd.data_ptr(), None, o4.data_ptr(), None]
+            + list(q4.shape[:3]) + [D, rot] + list(td.shape[:3])
+            + list(q4.stride()) + list(z4) + list(o4.stride()) + list(z4) + list(td.stride())
+            + [wd.stride(0), 0, 1e-5, 2, 2, 2, False, True, torch.cuda.current_stream().cuda_stream])
+    assert len(args) == 46
+    _lib.load().launch_rms_rope_kernel(*args)
+    torch.cuda.synchronize()
+    want = cpu_ref.rms_rope_split_half1(x.unsqueeze(0), tab, w, 1e-5, rot)[0]
+    assert same(out, want, "launcher output")

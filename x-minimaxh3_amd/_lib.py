@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
                                c_void_p]),
     "xmh3_rms_adaln": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p,
                                c_void_p, c_int, c_i64, c_void_p, c_i64, c_float, c_void_p]),
+    "launch_rms_rope_kernel": (None, [c_void_p] * 7 + [c_i64] * 32 + [c_float] + [c_int] * 3 + [ctypes.c_bool] * 2
+                               + [c_void_p]),
     "xmh3_rope_split_half": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, P_I64, P_I64,
                                      c_void_p, c_int, c_void_p, c_int, P_I64, c_int, c_float, c_int, c_void_p]),
 }

@@ -1066,6 +1066,49 @@ extern "C" int xmh3_rms_adaln(const void* x, void* out, int dtype, int64_t rows,
                               mod_dtype, mod_ld, row_map, mod_group, eps, stream);
 }
 
+// The reference's 46-argument launcher, same name and argument list, so a
+// ctypes caller with pinned argtypes binds this library unchanged. It returns
+// nothing, as the reference's does: an argument this build does not take
+// (interleaved pairs, a non-contiguous last dimension, a strided weight or
+// table pair layout) launches nothing and leaves the message in
+// xmh3_last_error(). Size-1 table dimensions broadcast.
+extern "C" void launch_rms_rope_kernel(
+    const void* q, const void* k, const void* freqs, const void* q_scale, const void* k_scale, void* q_out,
+    void* k_out, int64_t batch, int64_t dim1, int64_t dim2, int64_t head_dim, int64_t rot_dim,
+    int64_t freqs_batch, int64_t freqs_dim1, int64_t freqs_dim2, int64_t q_s0, int64_t q_s1, int64_t q_s2,
+    int64_t q_s3, int64_t k_s0, int64_t k_s1, int64_t k_s2, int64_t k_s3, int64_t qo_s0, int64_t qo_s1,
+    int64_t qo_s2, int64_t qo_s3, int64_t ko_s0, int64_t ko_s1, int64_t ko_s2, int64_t ko_s3, int64_t f_s0,
+    int64_t f_s1, int64_t f_s2, int64_t f_s3, int64_t f_s4, int64_t f_s5, int64_t qs_stride, int64_t ks_stride,
+    float epsilon, int input_dtype_code, int freqs_dtype_code, int scale_dtype_code, bool has_k,
+    bool split_half, hipStream_t stream) {
+  using namespace xmh3;
+  auto reject = [](const char* msg) { fail(XMH3_EUNSUPPORTED, msg); };
+  if (!split_half) return reject("launch_rms_rope_kernel: only the split-half pair layout is supported");
+  if (q_s3 != 1 || qo_s3 != 1 || (has_k && (k_s3 != 1 || ko_s3 != 1)))
+    return reject("launch_rms_rope_kernel: the head dimension must be contiguous");
+  if (f_s5 != 1 || f_s4 != 2 || f_s3 != 4)
+    return reject("launch_rms_rope_kernel: table pairs must be contiguous [rot/2, 2, 2]");
+  if ((q_scale && qs_stride != 1) || (has_k && k_scale && ks_stride != 1))
+    return reject("launch_rms_rope_kernel: the norm weights must be contiguous");
+  if ((freqs_batch != 1 && freqs_batch != batch) || (freqs_dim1 != 1 && freqs_dim1 != dim1) ||
+      (freqs_dim2 != 1 && freqs_dim2 != dim2))
+    return reject("launch_rms_rope_kernel: table dimensions must be 1 or match the input");
+  const int64_t fst[3] = {freqs_batch == 1 ? 0 : f_s0, freqs_dim1 == 1 ? 0 : f_s1, freqs_dim2 == 1 ? 0 : f_s2};
+  const int norm = q_scale != nullptr;
+  {
+    const int64_t xs[3] = {q_s0, q_s1, q_s2}, os[3] = {qo_s0, qo_s1, qo_s2};
+    if (rope_heads(const_cast<void*>(q), q_out, input_dtype_code, batch, dim1, dim2, head_dim, xs, os, q_scale,
+                   scale_dtype_code, freqs, freqs_dtype_code, fst, (int)rot_dim, epsilon, norm, stream) != XMH3_OK)
+      return;
+  }
+  if (has_k) {
+    const int64_t xs[3] = {k_s0, k_s1, k_s2}, os[3] = {ko_s0, ko_s1, ko_s2};
+    rope_heads(const_cast<void*>(k), k_out, input_dtype_code, batch, dim1, dim2, head_dim, xs, os,
+               k_scale ? k_scale : q_scale, scale_dtype_code, freqs, freqs_dtype_code, fst, (int)rot_dim, epsilon,
+               k_scale ? 1 : norm, stream);
+  }
+}
+
 extern "C" int xmh3_rope_split_half(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H,
                                     int64_t head_dim, const int64_t* x_strides,
                                     const int64_t* out_strides, const void* norm_weight,
