@@ -58,15 +58,20 @@ __device__ __forceinline__ float g8(const V8<T>& d, int j) {
     return __uint_as_float((&d.v[j >> 2].x)[j & 3]);
   }
 }
+// 8 fp32 values rounded to T's storage, two per conversion for 16-bit T
 template <typename T>
-__device__ __forceinline__ void s8(V8<T>& d, int j, float f) {
+__device__ __forceinline__ V8<T> pack8(const float* y) {
+  V8<T> d;
   if constexpr (sizeof(typename T::storage) == 2) {
-    uint32_t& w = (&d.v.x)[j >> 1];
-    uint32_t b = T::store(f);
-    w = (j & 1) ? ((w & 0xffffu) | (b << 16)) : ((w & 0xffff0000u) | b);
+    d.v = make_uint4(T::store2(y[0], y[1]), T::store2(y[2], y[3]), T::store2(y[4], y[5]),
+                     T::store2(y[6], y[7]));
   } else {
-    (&d.v[j >> 2].x)[j & 3] = __float_as_uint(f);
+    d.v[0] = make_uint4(__float_as_uint(y[0]), __float_as_uint(y[1]), __float_as_uint(y[2]),
+                        __float_as_uint(y[3]));
+    d.v[1] = make_uint4(__float_as_uint(y[4]), __float_as_uint(y[5]), __float_as_uint(y[6]),
+                        __float_as_uint(y[7]));
   }
+  return d;
 }
 
 // type promotion of (x dtype, modulation dtype) as torch does for x * (1 + s)
@@ -372,10 +377,7 @@ __global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
         *reinterpret_cast<uint4*>(ob + o0) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
         *reinterpret_cast<uint4*>(ob + o1) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
       } else {
-        V8<TO> ov;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s8<TO>(ov, j, y[t][0][j]);
-        st8<TO>(t ? a.o1 : a.o0, row * a.ldo + o0, ov);
+        st8<TO>(t ? a.o1 : a.o0, row * a.ldo + o0, pack8<TO>(y[t][0]));
       }
     }
   }
@@ -608,9 +610,34 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
 // ---------------------------------------------------------------------------
 // head-span kernel: LPH lanes per (b, s, h) head
 // ---------------------------------------------------------------------------
+// Division of non-negative 64-bit values by a launch-invariant divisor d >= 1
+// with a precomputed multiplier (Granlund & Montgomery, "Division by
+// invariant integers using multiplication", PLDI 1994, the round-up form):
+// l = ceil(log2 d), m = floor(2^64 (2^l - d) / d) + 1,
+// q = (t + ((n - t) >> 1)) >> (l - 1) with t = mulhi(m, n); d == 1 is q = n.
+struct FastDivU64 {
+  uint64_t d, m;
+  int l;
+  static FastDivU64 make(uint64_t d) {
+    FastDivU64 f{d, 0, 0};
+    while (f.l < 64 && (uint64_t(1) << f.l) < d) ++f.l;
+    if (d > 1) {
+      const unsigned __int128 two_l = (unsigned __int128)1 << f.l;
+      f.m = (uint64_t)((((two_l - d) << 64) / d) + 1);
+    }
+    return f;
+  }
+  __device__ __forceinline__ uint64_t div(uint64_t n) const {
+    if (d == 1) return n;
+    const uint64_t t = __umul64hi(m, n);
+    return (t + ((n - t) >> 1)) >> (l - 1);
+  }
+};
+
 struct HeadArgs {
   void* x; void* out;                 // out may alias x (in place)
   int64_t B, S, H, D;
+  FastDivU64 divS, divH;              // by S and by H
   int64_t sb, ss, sh;                 // element strides of x
   int64_t ob, os, oh;                 // element strides of out
   const void* weight;                 // [D] (NORM)
@@ -623,23 +650,36 @@ struct HeadArgs {
 // TABL: the table is shared by the heads of a token (head stride 0) and the
 // block's heads span at most 8 tokens; the block stages those table rows in
 // LDS once instead of every pair lane reading its 128 bytes from L2.
+// Pair lane s owns TAB_CPL 16-byte chunks of a staged row; its chunk k is
+// stored at slot (k - s) mod TAB_CPL of its segment, so at each read step the
+// lanes of a group touch different banks.
 template <typename TF>
-__device__ __forceinline__ void lds_tab8(const uint8_t* p, Tab8<TF>& t) {
-  V8<TF> raw[4];
+constexpr int tab_cpl() { return 8 * 4 * (int)sizeof(typename TF::storage) / 16; }
+template <typename TF>
+__device__ __forceinline__ int tab_slot(int c) {   // chunk c of a row -> stored chunk
+  constexpr int CPL = tab_cpl<TF>();
+  const int seg = c / CPL, k = c - seg * CPL;
+  return seg * CPL + ((k - seg) & (CPL - 1));
+}
+template <typename TF>
+__device__ __forceinline__ void lds_tab8(const uint8_t* row, int seg, Tab8<TF>& t) {
+  constexpr int CPL = tab_cpl<TF>();
+  const uint8_t* p = row + seg * CPL * 16;
+  uint4 raw[CPL];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const uint8_t* pq = p + q * 8 * (int)sizeof(typename TF::storage);
-    if constexpr (sizeof(typename TF::storage) == 4) {
-      raw[q].v[0] = *reinterpret_cast<const uint4*>(pq);
-      raw[q].v[1] = *reinterpret_cast<const uint4*>(pq + 16);
-    } else {
-      raw[q].v = *reinterpret_cast<const uint4*>(pq);
-    }
-  }
+  for (int k = 0; k < CPL; ++k) raw[k] = *reinterpret_cast<const uint4*>(p + ((k - seg) & (CPL - 1)) * 16);
 #pragma unroll
   for (int pp = 0; pp < 8; ++pp)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) t.f[pp][e] = g8<TF>(raw[(pp * 4 + e) >> 3], (pp * 4 + e) & 7);
+    for (int e = 0; e < 4; ++e) {
+      const int idx = pp * 4 + e;     // element of the lane's 32
+      if constexpr (sizeof(typename TF::storage) == 4) {
+        t.f[pp][e] = __uint_as_float((&raw[idx >> 2].x)[idx & 3]);
+      } else {
+        const uint32_t w = (&raw[idx >> 3].x)[(idx & 7) >> 1];
+        t.f[pp][e] = TF::load((idx & 1) ? (w >> 16) : (w & 0xffffu));
+      }
+    }
 }
 
 constexpr int HEAD_TAB_ROWS = 8, HEAD_TAB_ROW_BYTES = 1024;   // rot <= 128, fp32
@@ -654,7 +694,8 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
   // compute on a clamped head and skip the stores
   const bool live = head < nheads;
   const int64_t hd = live ? head : 0;
-  const int64_t h = hd % a.H, bs = hd / a.H, s = bs % a.S, b = bs / a.S;
+  const int64_t bs = (int64_t)a.divH.div((uint64_t)hd), h = hd - bs * a.H;
+  const int64_t b = (int64_t)a.divS.div((uint64_t)bs), s = bs - b * a.S;
   const int half = a.rot >> 1;
   const int pair_items = half / 8;
   const int tail_items = (int)((a.D - a.rot) / 8);
@@ -692,15 +733,15 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     const int chunks = row_bytes / 16;
     for (int i = threadIdx.x; i < nrow * chunks; i += 256) {
       const int rrow = i / chunks, c = i - rrow * chunks;
-      const int64_t bsr = bs0 + rrow, sr = bsr % a.S, br = bsr / a.S;
+      const int64_t bsr = bs0 + rrow, br = (int64_t)a.divS.div((uint64_t)bsr), sr = bsr - br * a.S;
       const uint8_t* src = static_cast<const uint8_t*>(a.freqs) +
                            (br * a.fb + sr * a.fs) * (int64_t)sizeof(typename TF::storage);
-      *reinterpret_cast<uint4*>(tabs + rrow * HEAD_TAB_ROW_BYTES + c * 16) =
+      *reinterpret_cast<uint4*>(tabs + rrow * HEAD_TAB_ROW_BYTES + tab_slot<TF>(c) * 16) =
           *reinterpret_cast<const uint4*>(src + c * 16);
     }
     __syncthreads();
     if (is_pair && live)
-      lds_tab8<TF>(tabs + (bs - bs0) * HEAD_TAB_ROW_BYTES + it * 8 * 4 * (int)sizeof(typename TF::storage), tab);
+      lds_tab8<TF>(tabs + (bs - bs0) * HEAD_TAB_ROW_BYTES, it, tab);
   } else {
     if (is_pair) load_tab8<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 8 * 4, tab);
   }
@@ -710,7 +751,9 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     // the head is staged in LDS, lane g of the group walks chains
     // L = g, g + LPH, ... (32 chains, each over positions 32*i + L), then the
     // chain totals are combined row-wise and lane by lane.
-    __shared__ __attribute__((aligned(16))) typename TX::storage heads[256 / LPH][16 * LPH];
+    // rows padded by 16 bytes: the groups of a wave start 4 banks apart
+    constexpr int HROW = 16 * LPH + 16 / (int)sizeof(typename TX::storage);
+    __shared__ __attribute__((aligned(16))) typename TX::storage heads[256 / LPH][HROW];
     typename TX::storage* hrow = heads[threadIdx.x / LPH];
     if (is_pair || is_tail) {
       st8<TX>(hrow, c0, v0);
@@ -770,28 +813,30 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
   }
   if (!live || !(is_pair || is_tail)) return;
 
-  auto normalise = [&](V8<TX>& vv, const V8<TW>& wv) {
-    if constexpr (NORM) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s8<TX>(vv, j, TX::round((g8<TX>(vv, j) * rr) * g8<TW>(wv, j)));
-    }
-  };
-  normalise(v0, wv0);
-  if (is_pair) {
-    normalise(v1, wv1);
-    V8<TX> r0, r1;
+  // element pass in fp32: each element is unpacked once, rounded where the
+  // eager op order rounds, and packed two per conversion on the way out (the
+  // pack rounds to x's dtype, which is the rotation's last rounding)
+  float y0[8], y1[8];
+  auto normalise = [&](const V8<TX>& vv, const V8<TW>& wv, float* y) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      float y0, y1;
-      rotate_pair<TF, TX>(g8<TX>(v0, j), g8<TX>(v1, j), tab.f[j][0], tab.f[j][1], tab.f[j][2],
-                          tab.f[j][3], y0, y1);
-      s8<TX>(r0, j, y0);
-      s8<TX>(r1, j, y1);
+      y[j] = g8<TX>(vv, j);
+      if constexpr (NORM) y[j] = TX::round((y[j] * rr) * g8<TW>(wv, j));
     }
-    st8<TX>(a.out, ooff + c0, r0);
-    st8<TX>(a.out, ooff + c1, r1);
+  };
+  normalise(v0, wv0, y0);
+  if (is_pair) {
+    normalise(v1, wv1, y1);
+    float r0[8], r1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      rotate_pair<TF, F32T>(y0[j], y1[j], tab.f[j][0], tab.f[j][1], tab.f[j][2], tab.f[j][3], r0[j], r1[j]);
+    st8<TX>(a.out, ooff + c0, pack8<TX>(r0));
+    st8<TX>(a.out, ooff + c1, pack8<TX>(r1));
+  } else if constexpr (NORM) {
+    st8<TX>(a.out, ooff + c0, pack8<TX>(y0));
   } else {
-    st8<TX>(a.out, ooff + c0, v0);
+    st8<TX>(a.out, ooff + c0, v0);      // pass-through dims keep their bits
   }
 }
 
@@ -1023,6 +1068,7 @@ int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, i
   a.sb = xstrides[0]; a.ss = xstrides[1]; a.sh = xstrides[2];
   a.ob = ostrides[0]; a.os = ostrides[1]; a.oh = ostrides[2];
   a.weight = weight; a.freqs = freqs; a.fb = fstrides[0]; a.fs = fstrides[1]; a.fh = fstrides[2];
+  a.divS = FastDivU64::make((uint64_t)S); a.divH = FastDivU64::make((uint64_t)H);
   a.rot = rot; a.eps = eps;
   XMH3_REQUIRE(!norm || weight_dtype == dtype || weight_dtype == DT_F32,
                "rope: norm weight must have x's dtype or fp32");
