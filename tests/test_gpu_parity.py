@@ -850,3 +850,41 @@ def test_reference_named_rope_launcher(pkg, dev, hnd_out):
     torch.cuda.synchronize()
     want = cpu_ref.rms_rope_split_half1(x.unsqueeze(0), tab, w, 1e-5, rot)[0]
     assert same(out, want, "launcher output")
+
+
+def test_empty_token_batches(pkg, dev):
+    """A batch of zero tokens returns empty results with the oracle's shapes
+    and dtypes (no kernel is launched for an empty grid)."""
+    say("empty token batches")
+    g = torch.Generator().manual_seed(41)
+    x = torch.empty(0, 512, dtype=torch.bfloat16)
+    w1 = torch.randint(-127, 128, (256, 512), generator=g, dtype=torch.int8)
+    s1 = torch.rand(256, generator=g) * 1e-2
+    w2 = torch.randint(-127, 128, (512, 256), generator=g, dtype=torch.int8)
+    s2 = torch.rand(512, generator=g) * 1e-2
+    scale = torch.zeros(1, 512, dtype=torch.bfloat16)
+    shift = torch.zeros(1, 512, dtype=torch.bfloat16)
+
+    def check(got, want, what):
+        got = got if isinstance(got, tuple) else (got,)
+        want = want if isinstance(want, tuple) else (want,)
+        for a, b in zip(got, want):
+            say(f"  {what}: {tuple(a.shape)} {a.dtype}")
+            assert a.is_cuda and tuple(a.shape) == tuple(b.shape) and a.dtype == b.dtype, (what, a.shape, b.shape)
+
+    from x_minimaxh3_amd import backend
+
+    xd = x.to(dev)
+    check(pkg.quantize_int8_rowwise(xd), cpu_ref.quantize_int8_rowwise(x), "quantize_int8_rowwise")
+    check(backend.quantize_int8_rowwise_convrot64(xd, 256), cpu_ref.quantize_convrot(x, 256)[:2],
+          "convrot quantizer")
+    check(pkg.int8_linear(xd, w1.to(dev), s1.to(dev)), cpu_ref.int8_linear(x, w1, s1), "int8_linear")
+    check(pkg.w8a8_mlp(xd, w1.to(dev), s1.to(dev), w2.to(dev), s2.to(dev)),
+          cpu_ref.w8a8_mlp(x, w1, s1, w2, s2), "w8a8_mlp")
+    check(pkg.rms_adaln(xd, scale.to(dev), shift.to(dev)), cpu_ref.rms_adaln(x, scale, shift), "rms_adaln")
+    tab = torch.zeros(1, 1, 1, 64, 2, 2)
+    qo, ko = pkg.norm_rope(xd, xd, scale.to(dev), shift.to(dev), tab.to(dev), 1e-6, 128)
+    # the eager rope's reshape(..., 2, -1) raises on zero elements, so the
+    # oracle gives no shape here; the fused op returns Q's and K's empty shape
+    check((qo, ko), (x, x), "norm_rope")
+    torch.cuda.synchronize()
