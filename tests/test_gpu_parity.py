@@ -489,7 +489,9 @@ def test_h3_qknorm_rope_partial_inplace(pkg, dev):
 def test_rms_adaln(pkg, dev, mod_dtype):
     say(f"rms_adaln scale/shift {mod_dtype}")
     g = torch.Generator().manual_seed(23)
-    x = torch.randn(2, 300, 5120, generator=g).to(torch.bfloat16)
+    # 301 tokens per sample: with one block of rows per CU, a block straddles
+    # the sample boundary, so both modulation sources of the kernel run
+    x = torch.randn(2, 301, 5120, generator=g).to(torch.bfloat16)
     sc = (torch.randn(2, 1, 5120, generator=g) * 0.1).to(mod_dtype)
     sh = (torch.randn(2, 1, 5120, generator=g) * 0.1).to(mod_dtype)
     out = pkg.rms_adaln(x.to(dev), sc.to(dev), sh.to(dev), 1e-6)
@@ -500,16 +502,21 @@ def test_rms_adaln(pkg, dev, mod_dtype):
     assert same(out, want, "rms_adaln")
 
 
-def test_h3_segmented_rms_adaln(pkg, dev):
-    say("h3 segmented rms_adaln")
+@pytest.mark.parametrize("rows,width,segs", [
+    (1000, 1024, ((0, 77, 0), (77, 200, 1), (200, 1000, 2))),
+    # H3's width (672 8-element items: the last 64-item step is half full),
+    # segment boundaries inside blocks of rows
+    (1500, 5376, ((0, 101, 0), (101, 513, 1), (513, 1500, 2))),
+])
+def test_h3_segmented_rms_adaln(pkg, dev, rows, width, segs):
+    say(f"h3 segmented rms_adaln rows={rows} width={width}")
     from x_minimaxh3_amd import h3
 
     g = torch.Generator().manual_seed(24)
-    x = torch.randn(1000, 1024, generator=g).to(torch.bfloat16)
-    w = (torch.rand(1024, generator=g) + 0.5).to(torch.bfloat16)
-    sc = (torch.randn(3, 1024, generator=g) * 0.1).to(torch.bfloat16)
-    sh = (torch.randn(3, 1024, generator=g) * 0.1).to(torch.bfloat16)
-    segs = ((0, 77, 0), (77, 200, 1), (200, 1000, 2))
+    x = torch.randn(rows, width, generator=g).to(torch.bfloat16)
+    w = (torch.rand(width, generator=g) + 0.5).to(torch.bfloat16)
+    sc = (torch.randn(3, width, generator=g) * 0.1).to(torch.bfloat16)
+    sh = (torch.randn(3, width, generator=g) * 0.1).to(torch.bfloat16)
     out = h3.rms_adaln(x.to(dev), w.to(dev), sh.to(dev), sc.to(dev), segs, eps=1e-5)
     torch.cuda.synchronize()
     want = cpu_ref.rms_adaln_segmented(x, w, sh, sc, segs, eps=1e-5)

@@ -608,6 +608,162 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined rms_adaln (row-span, no rotation) for 16-bit rows whose
+// modulation has the rows' dtype.
+//
+// Block b owns the contiguous rows [b * chunk, (b + 1) * chunk); its waves take
+// rows first + wave, first + wave + WPB, ..., two rows ahead, as in the
+// norm-rope pipe kernel above. The block caches in LDS round(1 + scale), shift
+// and the norm weight of its first row's modulation row; a row with another
+// modulation row (a block that straddles a segment or sample boundary) reads
+// its modulation from global memory, which costs that row the prefetch
+// overlap. Item slots u = s * 64 + lane (s < NSTEP) are clamped to the last
+// item, so every lane issues the same unpredicated loads and stores (a
+// clamped lane recomputes and rewrites the last item's identical bytes).
+//
+// LDS: 3 * D * sizeof(x) (t, shift, weight) + WPB * D * sizeof(x).
+// ---------------------------------------------------------------------------
+template <typename TX, bool WEIGHT, int NSTEP>
+__global__ __launch_bounds__(512) void adaln_pipe_kernel(RowArgs a, int64_t chunk) {
+  using S = typename TX::storage;
+  static_assert(sizeof(S) == 2, "16-bit rows");
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+  const int D = (int)a.D, items = D >> 3;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wpb = blockDim.x >> 6;
+  S* lt = reinterpret_cast<S*>(dyn_lds);
+  S* lsh = lt + D;
+  S* lw = lsh + D;
+  S* lrow = lw + D + wave * D;
+  const int64_t first = (int64_t)blockIdx.x * chunk;
+  const int64_t last = first + chunk < a.rows ? first + chunk : a.rows;
+  if (first >= last) return;   // the whole block
+  auto mod_row = [&](int64_t row) -> int64_t {
+    return a.row_map ? (int64_t)a.row_map[row] : row / a.mod_group;
+  };
+  const int64_t m0 = mod_row(first);
+  {
+    const S* sc = static_cast<const S*>(a.scale) + m0 * a.mod_ld;
+    const S* sh = static_cast<const S*>(a.shift) + m0 * a.mod_ld;
+    for (int i = threadIdx.x; i < items; i += blockDim.x) {
+      V8<TX> vs, vh;
+      ld8<TX>(sc, (int64_t)i * 8, vs);
+      ld8<TX>(sh, (int64_t)i * 8, vh);
+      float t[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[j] = TX::round(1.0f + g8<TX>(vs, j));   // (1 + scale) in its dtype
+      st8<TX>(lt, (int64_t)i * 8, pack8<TX>(t));
+      st8<TX>(lsh, (int64_t)i * 8, vh);
+      if constexpr (WEIGHT) {
+        V8<TX> vw;
+        ld8<TX>(a.weight, (int64_t)i * 8, vw);
+        st8<TX>(lw, (int64_t)i * 8, vw);
+      }
+    }
+    __syncthreads();
+  }
+  int64_t r = first + wave;
+  if (r >= last) return;
+  const int64_t stride = wpb;
+  auto col = [&](int s) { const int u = s * 64 + lane; return (u < items ? u : items - 1) * 8; };
+
+  auto issue = [&](int64_t row, u32x4 (&bx)[NSTEP]) __attribute__((always_inline)) {
+    row = row < last ? row : last - 1;   // past the block's rows: re-read the last, never processed
+    const S* xb = static_cast<const S*>(a.x0) + row * a.ldx;
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s)   // streamed once: non-temporal
+      bx[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + col(s)));
+  };
+
+  // one item: rms_norm (x * rrms * w, rounded to x's dtype), then * t and
+  // + shift, each rounded, as the eager op order does
+  auto element = [&](int s, float rr, const float* t8, const float* sh8, S* ob) __attribute__((always_inline)) {
+    V8<TX> xv, wv;
+    xv.v = *reinterpret_cast<const uint4*>(lrow + col(s));
+    if constexpr (WEIGHT) wv.v = *reinterpret_cast<const uint4*>(lw + col(s));
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      float n0 = g8<TX>(xv, j) * rr, n1 = g8<TX>(xv, j + 1) * rr;
+      if constexpr (WEIGHT) { n0 = n0 * g8<TX>(wv, j); n1 = n1 * g8<TX>(wv, j + 1); }
+      TX::round2(n0, n1);
+      n0 = n0 * t8[j]; n1 = n1 * t8[j + 1];
+      TX::round2(n0, n1);
+      n0 = n0 + sh8[j]; n1 = n1 + sh8[j + 1];
+      TX::round2(n0, n1);
+      y[j] = n0;
+      y[j + 1] = n1;
+    }
+    const V8<TX> ov = pack8<TX>(y);
+    __builtin_nontemporal_store(u32x4{ov.v.x, ov.v.y, ov.v.z, ov.v.w}, reinterpret_cast<u32x4*>(ob + col(s)));
+  };
+
+  auto process = [&](int64_t row, u32x4 (&bx)[NSTEP]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < NSTEP; ++s) *reinterpret_cast<u32x4*>(lrow + col(s)) = bx[s];
+    // the buffer is free again: loads of row i+2, kept in program order
+    // (ahead of this row's stores) so the next wait can leave them in flight
+    __builtin_amdgcn_sched_barrier(0);
+    issue(row + 2 * stride, bx);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS stores done
+    __builtin_amdgcn_wave_barrier();
+    const float tot = ref_order_sumsq<TX>(lrow, D, lane);
+    const float rr = 1.0f / sqrtf(tot / (float)D + a.eps);
+    const int64_t m = mod_row(row);
+    S* ob = static_cast<S*>(a.o0) + row * a.ldo;
+    if (m == m0) {
+#pragma unroll
+      for (int s = 0; s < NSTEP; ++s) {
+        V8<TX> vt, vh;
+        vt.v = *reinterpret_cast<const uint4*>(lt + col(s));
+        vh.v = *reinterpret_cast<const uint4*>(lsh + col(s));
+        float t8[8], sh8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { t8[j] = g8<TX>(vt, j); sh8[j] = g8<TX>(vh, j); }
+        element(s, rr, t8, sh8, ob);
+      }
+    } else {
+      const S* sc = static_cast<const S*>(a.scale) + m * a.mod_ld;
+      const S* sh = static_cast<const S*>(a.shift) + m * a.mod_ld;
+#pragma unroll
+      for (int s = 0; s < NSTEP; ++s) {
+        V8<TX> vs, vh;
+        ld8<TX>(sc, col(s), vs);
+        ld8<TX>(sh, col(s), vh);
+        float t8[8], sh8[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) { t8[j] = TX::round(1.0f + g8<TX>(vs, j)); sh8[j] = g8<TX>(vh, j); }
+        element(s, rr, t8, sh8, ob);
+      }
+    }
+    // the next row's staging overwrites this wave's LDS slice: every lane's
+    // reads of it must be done
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // first row peeled off the loop, as in the norm-rope pipe kernel, so that
+  // the loop is entered with the memory operations of its back edge in flight
+  u32x4 x0[NSTEP], x1[NSTEP];
+  issue(r, x0);
+  issue(r + stride, x1);
+  __builtin_amdgcn_sched_barrier(0);
+  process(r, x0);
+  r += stride;
+  while (r < last) {
+    process(r, x1);
+    r += stride;
+    if (r >= last) break;
+    process(r, x0);
+    r += stride;
+  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): no load lands after the wave ends
+}
+
+// ---------------------------------------------------------------------------
 // head-span kernel: LPH lanes per (b, s, h) head
 // ---------------------------------------------------------------------------
 // Division of non-negative 64-bit values by a launch-invariant divisor d >= 1
@@ -924,6 +1080,40 @@ static int launch_pipe_n(RowArgs& a, int nt, hipStream_t st) {
   return check_launch("norm_rope_pipe_kernel");
 }
 
+// Launch of the pipelined rms_adaln kernel, one block of rows per CU.
+// Returns -1 (no launch) when the row does not fit its LDS plan.
+template <typename TX, bool WEIGHT, int N>
+static int launch_adaln_pipe_n(RowArgs& a, hipStream_t st) {
+  const size_t row = (size_t)a.D * sizeof(typename TX::storage);
+  if (4 * row > LDS_BYTES) return -1;
+  const int wpb = (int)std::min<size_t>(8, (LDS_BYTES - 3 * row) / row);
+  const size_t lds = (3 + (size_t)wpb) * row;
+  auto kern = adaln_pipe_kernel<TX, WEIGHT, N>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES) !=
+        hipSuccess)
+      return fail(XMH3_EHIP, "rms_adaln kernel: cannot raise the dynamic LDS limit");
+    attr_set = true;
+  }
+  const int64_t cus = std::max(1, cu_count());
+  const int64_t chunk = (a.rows + cus - 1) / cus;
+  const int64_t grid = (a.rows + chunk - 1) / chunk;
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * wpb), lds, st, a, chunk);
+  return check_launch("adaln_pipe_kernel");
+}
+
+template <typename TX, bool WEIGHT>
+static int launch_adaln_pipe(RowArgs& a, hipStream_t st) {
+  if (a.x1 || a.D % 8 != 0 || a.D >= (1 << 17)) return -1;
+  const int64_t steps = (a.D / 8 + 63) / 64;
+#define XMH3_AP(N) \
+  if (steps <= N) return launch_adaln_pipe_n<TX, WEIGHT, N>(a, st);
+  XMH3_AP(2) XMH3_AP(4) XMH3_AP(6) XMH3_AP(8) XMH3_AP(10) XMH3_AP(11) XMH3_AP(12)
+#undef XMH3_AP
+  return -1;
+}
+
 template <typename TX, typename TF, bool ADALN>
 static int launch_pipe(RowArgs& a, int nt, hipStream_t st) {
   if (a.D % 1024 != 0) return -1;
@@ -1001,6 +1191,10 @@ int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D,
   a.x0 = x; a.o0 = out; a.ldx = ldx; a.ldo = ldo; a.rows = rows; a.D = D; a.weight = weight;
   a.scale = scale; a.shift = shift; a.mod_ld = mod_ld; a.row_map = row_map; a.mod_group = mod_group;
   a.eps = eps;
+  if (dtype == DT_BF16 && mod_dtype == DT_BF16) {
+    const int rc = weight ? launch_adaln_pipe<BF16T, true>(a, st) : launch_adaln_pipe<BF16T, false>(a, st);
+    if (rc != -1) return rc;
+  }
 #define XMH3_RA(TX, TM)                                                          \
   {                                                                              \
     if (weight) return launch_row<TX, TM, F32T, false, true, true, 1>(a, st);    \
