@@ -883,8 +883,8 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     constexpr int G = 256 / LPH;
     const int64_t first = (int64_t)blockIdx.x * G;
     const int64_t last = (first + G < nheads ? first + G : nheads) - 1;
-    const int64_t bs0 = first / a.H;
-    const int nrow = (int)(last / a.H - bs0 + 1);          // <= HEAD_TAB_ROWS (host)
+    const int64_t bs0 = (int64_t)a.divH.div((uint64_t)first);
+    const int nrow = (int)((int64_t)a.divH.div((uint64_t)last) - bs0 + 1);   // <= HEAD_TAB_ROWS (host)
     const int row_bytes = half * 4 * (int)sizeof(typename TF::storage);
     const int chunks = row_bytes / 16;
     for (int i = threadIdx.x; i < nrow * chunks; i += 256) {
