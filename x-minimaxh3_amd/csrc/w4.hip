@@ -69,6 +69,72 @@ __global__ __launch_bounds__(256) void w4_decode_kernel(const uint8_t* __restric
   *reinterpret_cast<uint4*>(out + n * K + k0) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// G % 32 == 0: 32 outputs (16 packed bytes) per thread, one group. The
+// 16-entry table is four words of int8 (byte c % 4 of word c / 4 = the value
+// of code c), each entry clamp(level * s_rel) rounded to an integer by the
+// 1.5 * 2^23 addition (clamping first changes nothing: the bounds are
+// integers). Four codes are looked up at once: the nibbles of two packed bytes
+// are spread to four bytes, v_perm picks each byte from the words of codes
+// 0-7 and of codes 8-15, and bit 3 of each code selects between them.
+// Threads are numbered across rows: thread t decodes chunk t % (K / 32) of
+// row t / (K / 32) (32-bit, checked on the host).
+__device__ __forceinline__ uint32_t w4_entry4(float l0, float l1, float l2, float l3, float s) {
+  const float m = 12582912.0f;   // 1.5 * 2^23
+  const uint32_t y0 = __float_as_uint(fminf(fmaxf(l0 * s, -127.0f), 127.0f) + m);
+  const uint32_t y1 = __float_as_uint(fminf(fmaxf(l1 * s, -127.0f), 127.0f) + m);
+  const uint32_t y2 = __float_as_uint(fminf(fmaxf(l2 * s, -127.0f), 127.0f) + m);
+  const uint32_t y3 = __float_as_uint(fminf(fmaxf(l3 * s, -127.0f), 127.0f) + m);
+  const uint32_t lo = __builtin_amdgcn_perm(y1, y0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm(y3, y2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// 4 int8 outputs from the 4 codes of bytes (sel0, sel1) of w: selector
+// 0x01010000 spreads bytes 0-1, 0x03030202 bytes 2-3
+template <uint32_t SPREAD>
+__device__ __forceinline__ uint32_t w4_lookup4(uint32_t w, const uint32_t (&lut)[4]) {
+  const uint32_t t = __builtin_amdgcn_perm(0u, w, SPREAD);            // b0 b0 b1 b1
+  const uint32_t codes = (t & 0x000f000fu) | ((t >> 4) & 0x0f000f00u);  // lo hi lo hi nibbles
+  const uint32_t sel = codes & 0x07070707u;
+  const uint32_t a = __builtin_amdgcn_perm(lut[1], lut[0], sel);       // codes 0-7
+  const uint32_t b = __builtin_amdgcn_perm(lut[3], lut[2], sel);       // codes 8-15
+  const uint32_t hib = (codes >> 3) & 0x01010101u;
+  const uint32_t mask = (hib << 8) - hib;                              // 0xff where code >= 8
+  return (b & mask) | (a & ~mask);
+}
+
+template <bool BF16_SREL>
+__global__ __launch_bounds__(256) void w4_decode32_kernel(const uint8_t* __restrict__ packed,
+                                                          const void* __restrict__ s_rel,
+                                                          const float* __restrict__ codebook,
+                                                          uint32_t total, uint32_t per_row, int64_t K,
+                                                          int64_t G, int8_t* __restrict__ out) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= total) return;
+  const uint32_t n = t / per_row;
+  const int64_t k0 = (int64_t)(t - n * per_row) * 32;
+  const float s = load_srel<BF16_SREL>(s_rel, (int64_t)n * (K / G) + k0 / G);
+  uint32_t lut[4];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float l[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) l[b] = codebook ? codebook[w * 4 + b] : (float)(w * 4 + b - 8);
+    lut[w] = w4_entry4(l[0], l[1], l[2], l[3], s);
+  }
+  const uint4 p = *reinterpret_cast<const uint4*>(packed + (int64_t)n * (K / 2) + k0 / 2);
+  const uint32_t pw[4] = {p.x, p.y, p.z, p.w};
+  uint32_t o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = w4_lookup4<0x01010000u>(pw[i], lut);
+    o[2 * i + 1] = w4_lookup4<0x03030202u>(pw[i], lut);
+  }
+  int8_t* dst = out + (int64_t)n * K + k0;
+  *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
+  *reinterpret_cast<uint4*>(dst + 16) = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
 // any G (>= 2, dividing K): one byte (two outputs) per thread
 template <bool BF16_SREL>
 __global__ __launch_bounds__(256) void w4_decode_generic_kernel(const uint8_t* __restrict__ packed,
@@ -98,6 +164,17 @@ int w4_decode(const uint8_t* packed, const void* s_rel, int s_rel_dtype, const f
   XMH3_REQUIRE(packed && s_rel && out, "w4_decode: null pointer");
   XMH3_REQUIRE(s_rel_dtype == DT_F32 || s_rel_dtype == DT_BF16, "w4_decode: s_rel must be fp32 or bf16");
   const bool bf = s_rel_dtype == DT_BF16;
+  const bool fast32 = (G % 32 == 0) && ((uintptr_t)packed % 16 == 0) && ((uintptr_t)out % 16 == 0) &&
+                      N * (K / 32) < (1LL << 31);
+  if (fast32) {
+    const uint32_t per_row = (uint32_t)(K / 32), total = (uint32_t)(N * (K / 32));
+    dim3 grid((total + 255) / 256);
+    if (bf)
+      hipLaunchKernelGGL(w4_decode32_kernel<true>, grid, dim3(256), 0, st, packed, s_rel, codebook, total, per_row, K, G, out);
+    else
+      hipLaunchKernelGGL(w4_decode32_kernel<false>, grid, dim3(256), 0, st, packed, s_rel, codebook, total, per_row, K, G, out);
+    return check_launch("w4_decode32_kernel");
+  }
   const bool fast = (G % 16 == 0) && ((uintptr_t)packed % 8 == 0) && ((uintptr_t)out % 16 == 0);
   if (fast) {
     const int64_t threads = N * (K / 16);
