@@ -925,13 +925,23 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
       const int L = it + c * LPH;
       float acc = 0.0f;
       if (L < 32) {
-        for (int i = 0; i < steps; ++i) {
-          const float x = TX::load(hrow[i * 32 + L]);
-          acc = add_sq<TX>(acc, x);
+        // D <= 16 * LPH (host), so at most LPH / 2 steps of 32 and 3 leftover
+        // vectors: fully unrolled, every read is issued before the first add
+        constexpr int MAXS = LPH / 2 < 16 ? LPH / 2 : 16;
+#pragma unroll
+        for (int i = 0; i < MAXS; ++i) {
+          if (i < steps) {
+            const float x = TX::load(hrow[i * 32 + L]);
+            acc = add_sq<TX>(acc, x);
+          }
         }
-        for (int q = steps * 4; q < (D >> 3); ++q) {  // leftover 8-lane vectors -> row 0
-          const float x = TX::load(hrow[q * 8 + (L & 7)]);
-          if (L < 8) acc = add_sq<TX>(acc, x);
+#pragma unroll
+        for (int e = 0; e < 3; ++e) {  // leftover 8-lane vectors -> row 0
+          const int q = steps * 4 + e;
+          if (q < (D >> 3)) {
+            const float x = TX::load(hrow[q * 8 + (L & 7)]);
+            if (L < 8) acc = add_sq<TX>(acc, x);
+          }
         }
       }
       tch[c] = acc;
