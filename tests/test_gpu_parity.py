@@ -509,6 +509,11 @@ def test_rms_adaln(pkg, dev, mod_dtype):
     # H3's width (672 8-element items: the last 64-item step is half full),
     # segment boundaries inside blocks of rows
     (1500, 5376, ((0, 101, 0), (101, 513, 1), (513, 1500, 2))),
+    # the widest row of the pipelined kernel, the first one past it (one row
+    # per wave), and a width whose last 64-item step holds one item
+    (300, 6144, ((0, 7, 0), (7, 150, 1), (150, 300, 2))),
+    (300, 6152, ((0, 7, 0), (7, 150, 1), (150, 300, 2))),
+    (257, 520, ((0, 3, 0), (3, 100, 1), (100, 257, 2))),
 ])
 def test_h3_segmented_rms_adaln(pkg, dev, rows, width, segs):
     say(f"h3 segmented rms_adaln rows={rows} width={width}")
