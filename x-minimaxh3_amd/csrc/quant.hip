@@ -182,6 +182,75 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// register-resident path for wide rows: two waves per row, wave w taking the
+// 512-element steps w, w + 2, w + 4, ... (NL each), so half the row's
+// registers per wave and more waves per SIMD to hide the loads; the two
+// partial maxima meet in LDS. Same per-element operations as the one-wave
+// path, and max is order-free, so the codes and scale are identical.
+// ---------------------------------------------------------------------------
+template <typename T, int ACT, int NL>
+__global__ __launch_bounds__(256) void quant_rows_reg2_kernel(
+    const typename T::storage* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale,
+    uint32_t* __restrict__ zero_rows) {
+  __shared__ float part_max[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = wave & 1;
+  const int64_t row = (int64_t)blockIdx.x * 2 + (wave >> 1);
+  const bool row_ok = row < M;
+  const typename T::storage* xr = x + (row_ok ? row : 0) * ldx;
+  Pack8<T> buf[NL];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int64_t col = ((int64_t)(2 * i + half) * 64 + lane) * 8;
+    if (row_ok && col < K) {
+      load8<T>(xr + col, buf[i]);
+      if constexpr (ACT == ACT_GELU_TANH && sizeof(typename T::storage) == 2) {
+#pragma unroll
+        for (int j = 0; j < 8; j += 2) {
+          const float g0 = gelu_tanh_f32(get8<T>(buf[i], j)), g1 = gelu_tanh_f32(get8<T>(buf[i], j + 1));
+          amax = fmaxf(amax, fmaxf(fabsf(g0), fabsf(g1)));
+          (&buf[i].v.x)[j >> 1] = T::store2(g0, g1);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float f = get8<T>(buf[i], j);
+          if constexpr (ACT == ACT_GELU_TANH) {
+            f = T::round(gelu_tanh_f32(f));
+            set8<T>(buf[i], j, f);
+          }
+          amax = fmaxf(amax, fabsf(f));
+        }
+      }
+    }
+  }
+  amax = wave_max(amax);
+  if (lane == 0) part_max[wave] = amax;
+  __syncthreads();
+  if (!row_ok) return;
+  amax = T::round(fmaxf(part_max[wave & 2], part_max[(wave & 2) + 1]));
+  const float s = row_scale(amax);
+  const float sT = scale_for_math<T>(s);
+  const float inv = 1.0f / sT;
+  int8_t* qr = q + row * ldq;
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int64_t col = ((int64_t)(2 * i + half) * 64 + lane) * 8;
+    if (col < K) {
+      const Pack8<T>& b = buf[i];
+      const uint32_t lo = quant_word4<T>(get8<T>(b, 0), get8<T>(b, 1), get8<T>(b, 2), get8<T>(b, 3), sT, inv);
+      const uint32_t hi = quant_word4<T>(get8<T>(b, 4), get8<T>(b, 5), get8<T>(b, 6), get8<T>(b, 7), sT, inv);
+      *reinterpret_cast<uint2*>(qr + col) = make_uint2(lo, hi);
+    }
+  }
+  if (lane == 0 && half == 0) {
+    scale[row] = s;
+    if (zero_rows) zero_rows[row] = 0u;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // generic path: one 256-thread block per row, two passes over the row
 // (any K; the second pass re-reads the row, mostly from L2)
 // ---------------------------------------------------------------------------
@@ -269,6 +338,17 @@ static int launch_quant_T(const void* x, int64_t ldx, int64_t M, int64_t K, int8
   const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) &&
                       ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
   const int64_t steps = (K + 511) / 512;
+  if (vec_ok && steps > 16 && steps <= 32 && M <= (1LL << 24)) {
+    dim3 grid((unsigned)((M + 1) / 2));
+#define XMH3_Q2(NLV)                                                                                 \
+  if ((steps + 1) / 2 <= NLV) {                                                                      \
+    hipLaunchKernelGGL((quant_rows_reg2_kernel<T, ACT, NLV>), grid, dim3(256), 0, st, xs, ldx, M, K, \
+                       q, ldq, scale, zero_rows);                                                    \
+    return check_launch("quant_rows_reg2_kernel");                                                   \
+  }
+    XMH3_Q2(10) XMH3_Q2(12) XMH3_Q2(14) XMH3_Q2(16)
+#undef XMH3_Q2
+  }
   if (vec_ok && steps <= 32) {
     dim3 grid((unsigned)((M + 3) / 4));
 #define XMH3_Q(NLV)                                                                                \
