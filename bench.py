@@ -50,9 +50,9 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 # 0.5 GiB by FETCH_SIZE and 1 GiB by WRITE_SIZE, so FETCH_SIZE is scaled x2 and
 # WRITE_SIZE x1 (see profiles/).
 TRAFFIC_BYTES = {
-    "fc1_gemm": (1445940.4 * 2 + 691097.1) * 1024,
-    "fc2_gemm": (1475246.1 * 2 + 255960.2) * 1024,
-    "norm_rope": (265136.6 * 2 + 504015.9) * 1024,
+    "fc1_gemm": (1460067.6 * 2 + 691096.8) * 1024,
+    "fc2_gemm": (1475146.7 * 2 + 255960.1) * 1024,
+    "norm_rope": (265152.6 * 2 + 504021.2) * 1024,
 }
 
 
