@@ -203,7 +203,9 @@ int xmh3_norm_rope(const void* q_in, void* q_out, const void* k_in, void* k_out,
 /*
  * rms_norm(x [* norm_weight]) * (1 + scale[r]) + shift[r], r = row_map[t]
  * (if non-NULL) else t / mod_group; output in torch's promoted dtype of
- * (x, scale).
+ * (x, scale). With a row map, mod_group is the number of rows of the scale /
+ * shift tables and map entries are clamped into [0, mod_group), so a bad map
+ * never reads outside the tables.
  * Replaces: CK/backends/cuda/ops/adaln.cu:256-313 (launcher of the
  * (RMS-)AdaLN kernels), eager CK/backends/eager/adaln.py:17-20; with
  * norm_weight and row_map the H3 segmented form

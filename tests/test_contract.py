@@ -170,3 +170,92 @@ def test_h3_w4a8_spec_and_loader(pkg, tmp_path):
         h3.load_w4a8_linear(bad, "blk.fc")
     with pytest.raises(ValueError):
         h3.load_w4a8_linear(loaded, "blk.fc", spec={"format": "asym_w4a8_int8", "group_size": 12})
+
+
+def test_constraints_carry_the_reference_validation_surface(pkg):
+    """Every capability entry exposes what CK/constraints.py:127-255 reads, so
+    the table registers in the reference registry unchanged, and the
+    reference's validation steps give the expected verdicts on it."""
+    import importlib
+
+    from x_minimaxh3_amd import backend
+    reg = importlib.import_module("x_minimaxh3_amd.registry")   # the package re-exports the instance as `registry`
+
+    caps = backend._capabilities()
+    assert caps
+    for name, c in caps.items():
+        assert hasattr(c, "min_compute_capability") and c.min_compute_capability is None
+        assert isinstance(c.default_devices, frozenset) and isinstance(c.call_rules, tuple)
+        for pname, pc in c.params.items():
+            for attr in ("dtypes", "devices", "shape_rules", "check_dtype", "check_device", "check_shape"):
+                assert hasattr(pc, attr), (name, pname, attr)
+            for rule in pc.shape_rules:
+                assert isinstance(rule, reg.ShapeRule) and rule.describe()
+    c = caps["int8_linear"]
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    assert c.params["x"].check_dtype(x) and not c.params["x"].check_dtype(torch.zeros(4, dtype=torch.int8))
+    assert not c.params["x"].check_device(x, c.default_devices)          # the input must be on the GPU
+    assert c.params["weight_scale"].check_device(x.float(), c.default_devices)   # small operands may not be
+    assert c.params["weight"].check_shape(torch.zeros(8, 64, dtype=torch.int8))
+    assert not c.params["weight"].check_shape(torch.zeros(8, dtype=torch.int8))
+    r = reg.validate_function_call(c, {"x": x}, (9, 5))
+    assert not r.success and r.failed_param == "x" and "device cpu" in r.failure_reason
+    need = reg.FunctionConstraints(params={}, min_compute_capability=(9, 5))
+    assert reg.validate_function_call(need, {}, (9, 5)).success
+    assert reg.validate_function_call(need, {}, (9, 4)).failed_param == "__hardware__"
+    assert reg.validate_function_call(need, {}, None).failed_param == "__hardware__"
+
+
+def test_host_tensors_raise_before_any_kernel_call(pkg, monkeypatch):
+    """A host tensor in a data, output or workspace slot raises ValueError
+    before the C ABI is reached (a host pointer handed to a kernel would fault
+    the GPU)."""
+    from x_minimaxh3_amd import backend
+
+    def no_call(*a, **k):
+        raise AssertionError("the C ABI was reached")
+
+    monkeypatch.setattr(backend, "call", no_call)
+    x = torch.randn(4, 256).bfloat16()
+    w8 = torch.zeros(8, 256, dtype=torch.int8)
+    tab = torch.zeros(1, 4, 1, 64, 2, 2)
+    q4 = torch.randn(1, 4, 2, 128).bfloat16()
+    cases = [
+        lambda: backend.quantize_int8_rowwise(x),
+        lambda: backend.int8_linear(x, w8, torch.ones(8)),
+        lambda: backend.w8a8_mlp(x, torch.zeros(512, 256, dtype=torch.int8), torch.ones(512),
+                                 torch.zeros(256, 512, dtype=torch.int8), torch.ones(256)),
+        lambda: backend.rms_adaln(x, x[:1], x[:1]),
+        lambda: backend.rms_adaln_rows(x, None, x[:2], x[:2], torch.zeros(4, dtype=torch.int32), 1e-5),
+        lambda: backend.norm_rope(x.reshape(4, 256), x.reshape(4, 256), x[:1], x[:1], tab, 1e-6, 128),
+        lambda: backend.apply_rope_split_half1_(q4, tab),
+        lambda: backend.rms_rope_split_half_(q4, q4.clone(), tab, torch.ones(128).bfloat16()),
+        lambda: backend.dequant_int4_grouped_to_int8(torch.zeros(8, 128, dtype=torch.int8),
+                                                     torch.ones(8, 2), None, 128),
+        lambda: backend.int8_linear_gated_residual_(x, w8, torch.ones(8), None, torch.zeros(4, 8).bfloat16(),
+                                                    torch.ones(1, 8), torch.zeros(4, dtype=torch.int32),
+                                                    convrot=False, input_act=None),
+    ]
+    for i, f in enumerate(cases):
+        with pytest.raises(ValueError, match="runs on the GPU"):
+            f()
+    # an output or workspace on another device than the input
+    meta = torch.empty(4, 256, dtype=torch.bfloat16, device="meta")
+    with pytest.raises(ValueError, match="out is on cpu"):
+        backend._same_device(meta.device, out=torch.empty(4, 256))
+
+
+def test_segment_rows_resolve_like_tensor_indexing(pkg):
+    """h3.segment_row_map with the table's row count resolves rows as the
+    reference's scale[row] does: negative rows count from the end, rows out
+    of range raise IndexError (never a read past the table)."""
+    from x_minimaxh3_amd import h3
+
+    m = h3.segment_row_map(10, ((0, 4, -1), (4, 10, 0)), "cpu", n_rows=3)
+    assert m.tolist() == [2] * 4 + [0] * 6
+    with pytest.raises(IndexError, match="out of bounds"):
+        h3.segment_row_map(10, ((0, 4, 3), (4, 10, 0)), "cpu", n_rows=3)
+    with pytest.raises(IndexError):
+        h3.segment_row_map(10, ((0, 4, -4), (4, 10, 0)), "cpu", n_rows=3)
+    with pytest.raises(ValueError, match="ordered partition"):
+        h3.segment_row_map(10, ((0, 4, 0), (5, 10, 0)), "cpu", n_rows=3)

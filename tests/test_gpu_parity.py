@@ -355,6 +355,37 @@ def test_w4a8_linear_and_mlp(pkg, dev):
     close(ym, ymr, "w4a8 mlp")
 
 
+def test_w4a8_mlp_720p_row_sample(pkg, dev):
+    """C4 at its full shape: 25,200 tokens, 5120 -> 13824 -> 5120, int4 group
+    128 (40 groups along fc1's K, 108 along fc2's), bf16 s_rel. Both linears
+    alone are bit-exact on sampled rows; the MLP is checked on 400 rows
+    including the last, partial row tile."""
+    say("w4a8 mlp 25200x5120x13824 g128")
+    from x_minimaxh3_amd import workloads
+
+    inp = workloads.mlp_inputs(**workloads.CONFIGS["mlp_720p"], seed=0, weights="w4a8")
+    names = ("w1_packed", "w1_srel", "w1_schannel", "w2_packed", "w2_srel", "w2_schannel")
+    w = {n: inp[n].to(dev) for n in names}
+    x = inp["x"]
+    g = torch.Generator().manual_seed(2)
+    rows = torch.cat((torch.randperm(25200 - 200, generator=g)[:200], torch.arange(25200 - 200, 25200)))
+    y = pkg.w4a8_mlp(x.to(dev), *(w[n] for n in names), 128).cpu()
+    yr = cpu_ref.w4a8_mlp(x[rows], inp["w1_packed"], inp["w1_srel"].float(), inp["w1_schannel"],
+                          inp["w2_packed"], inp["w2_srel"].float(), inp["w2_schannel"], 128)
+    close(y[rows], yr, "720p w4a8 mlp rows")
+    assert torch.isfinite(y.float()).all()
+    say("w4a8 linear K=5120 (40 groups) and K=13824 (108 groups)")
+    h = pkg.w4a8_int8_linear(x[rows].to(dev), w["w1_packed"], w["w1_srel"], w["w1_schannel"], group_size=128,
+                             convrot_groupsize=128, convrot=False).cpu()
+    assert same(h, cpu_ref.w4a8_linear(x[rows], inp["w1_packed"], inp["w1_srel"].float(), inp["w1_schannel"], 128),
+         "w4a8 fc1 rows")
+    x2 = (torch.randn(300, 13824, generator=g) * 0.3).to(torch.bfloat16)
+    y2 = pkg.w4a8_int8_linear(x2.to(dev), w["w2_packed"], w["w2_srel"], w["w2_schannel"], group_size=128,
+                              convrot_groupsize=128, convrot=False).cpu()
+    assert same(y2, cpu_ref.w4a8_linear(x2, inp["w2_packed"], inp["w2_srel"].float(), inp["w2_schannel"], 128),
+         "w4a8 fc2 rows")
+
+
 # --------------------------------------------------------------------------- norm / rope
 
 def test_norm_rope_720p(pkg, dev):
@@ -561,6 +592,55 @@ def test_long_driver_chunks_match_whole(pkg, dev):
     drv.run_streamed(q.pin_memory(), k.pin_memory(), inp["x"].pin_memory(), freqs, host["qo"], host["ko"], host["y"])
     assert torch.equal(host["qo"], wq.cpu()) and torch.equal(host["ko"], wk.cpu()) and torch.equal(host["y"], wy.cpu())
     close(host["y"], cpu_ref.w8a8_mlp(inp["x"], inp["w1"], inp["s1"], inp["w2"], inp["s2"]), "streamed mlp vs oracle")
+
+
+def test_long_grid_full_resident_and_streamed(pkg, dev):
+    """C5 at its full size: 130,560 tokens (16x68x120), d 5120, ffn 13824,
+    16,384-token chunks (seven full, one of 15,872). The streamed run equals
+    the resident run bit for bit, and every chunk's first, last and 22 random
+    rows meet the oracle (norm-rope bit-exact, MLP to the fp bar)."""
+    say("long grid 130560 tokens: inputs")
+    from x_minimaxh3_amd import driver, workloads
+
+    cfg = workloads.CONFIGS["long_16x68x120"]
+    m, d, f, chunk = 130560, cfg["d"], cfg["ffn"], cfg["chunk"]
+    wts = workloads.mlp_inputs(M=1, d=d, ffn=f, n_outlier=cfg["n_outlier"], seed=0)
+    w1, s1, w2, s2 = (wts[n].to(dev) for n in ("w1", "s1", "w2", "s2"))
+    gg = torch.Generator(device=dev).manual_seed(11)
+    q = torch.randn(m, d, generator=gg, device=dev).to(torch.bfloat16)
+    k = torch.randn(m, d, generator=gg, device=dev).to(torch.bfloat16)
+    xf = torch.randn(m, d, generator=gg, device=dev)
+    xf[:, wts["outliers"].to(dev)] *= 20.0
+    x = xf.to(torch.bfloat16)
+    del xf
+    gc = torch.Generator().manual_seed(12)
+    scale = (torch.randn(1, d, generator=gc) * 0.1).to(torch.bfloat16)
+    shift = (torch.randn(1, d, generator=gc) * 0.1).to(torch.bfloat16)
+    freqs_h = workloads.rope_table_3d(cfg["grid"])
+    freqs = freqs_h.to(dev)
+    drv = driver.LongBlockDriver(w1, s1, w2, s2, scale.to(dev), shift.to(dev), chunk=chunk)
+    say("long grid: resident run")
+    qo, ko, y = drv.run_resident(q, k, x, freqs)
+    torch.cuda.synchronize()
+    say("long grid: streamed run")
+    host_in = {n: t.cpu().pin_memory() for n, t in (("q", q), ("k", k), ("x", x))}
+    host_out = {n: torch.empty(m, d, dtype=torch.bfloat16, pin_memory=True) for n in ("qo", "ko", "y")}
+    drv.run_streamed(host_in["q"], host_in["k"], host_in["x"], freqs, host_out["qo"], host_out["ko"],
+                     host_out["y"])
+    assert torch.equal(host_out["qo"], qo.cpu()) and torch.equal(host_out["ko"], ko.cpu())
+    assert torch.equal(host_out["y"], y.cpu())
+    say("long grid: oracle on every chunk")
+    rows = []
+    for a in range(0, m, chunk):
+        b = min(m, a + chunk)
+        rows += [a, b - 1] + (a + torch.randperm(b - a - 2, generator=gc)[:22] + 1).tolist()
+    rows = torch.tensor(sorted(set(rows)))
+    assert rows[-1] == m - 1 and (rows >= 114688).sum() >= 24      # the 15,872-token tail is sampled
+    xq, xk, xx = host_in["q"][rows], host_in["k"][rows], host_in["x"][rows]
+    fr = freqs_h[:, rows]
+    assert same(host_out["qo"][rows], cpu_ref.norm_rope(xq, scale, shift, fr, 128, 1e-6), "long q rows")
+    assert same(host_out["ko"][rows], cpu_ref.norm_rope(xk, scale, shift, fr, 128, 1e-6), "long k rows")
+    close(host_out["y"][rows], cpu_ref.w8a8_mlp(xx, wts["w1"], wts["s1"], wts["w2"], wts["s2"]), "long mlp rows")
 
 
 # --------------------------------------------------------------------------- ConvRot / swiglu quantizer

@@ -412,3 +412,122 @@ def test_w4a8_correction_route_against_float_weight():
         for grp in range(4):
             total = torch.tensor(float(int(q[r, 16 * grp:16 * grp + 16].int().sum())))
             assert sums[r, grp].item() == (total * xs[r, 0]).item()      # one fp32 product
+
+
+# --------------------------------------------------------------------------- composites
+
+def _rand_scales(n, seed, lo=1e-4, hi=1e-3):
+    g = torch.Generator().manual_seed(seed)
+    return torch.rand(n, generator=g) * (hi - lo) + lo
+
+
+def _bf16_chain_linear(x_bits, w, sw):
+    """Step-by-step W8A8 linear on bit patterns: quantize (numpy rule), int64
+    matmul, fp32 dequant rounded once to bf16. Returns bf16 bits."""
+    q, s = npref.quantize_rows_bf16(x_bits)
+    acc = npref.int_mm(q, w)
+    return npref.dequant_bf16_bits(acc, s, sw)
+
+
+def test_w8a8_mlp_composite_step_by_step():
+    """cpu_ref.w8a8_mlp = fc1 int8 linear, GELU-tanh on the bf16 h (the library
+    routine on bf16, the reference's materialisation point), per-token requant,
+    fc2 int8 linear. A GELU applied to the fp32 accumulators, after the
+    requant, or a skipped bf16 rounding of h changes bits here."""
+    m, d, f = 64, 256, 512
+    x = outlier_acts(m, d, seed=31, n_out=4)
+    g = torch.Generator().manual_seed(32)
+    w1 = torch.randint(-127, 128, (f, d), generator=g, dtype=torch.int8)
+    w2 = torch.randint(-127, 128, (d, f), generator=g, dtype=torch.int8)
+    s1, s2 = _rand_scales(f, 33, 1e-4, 4e-4), _rand_scales(d, 34, 1e-4, 4e-4)
+    y = cpu_ref.w8a8_mlp(x, w1, s1, w2, s2)
+    h = _bf16_chain_linear(bits(x), w1.numpy(), s1.numpy())
+    gl = F.gelu(from_bits(h), approximate="tanh")
+    assert gl.dtype == torch.bfloat16
+    yn = _bf16_chain_linear(bits(gl), w2.numpy(), s2.numpy())
+    assert np.array_equal(bits(y), yn)
+    # the GELU input is h itself (not the fp32 accumulators): a chain that
+    # rounds GELU of the unrounded dequant differs somewhere
+    q1, sx1 = npref.quantize_rows_bf16(bits(x))
+    acc1 = npref.int_mm(q1, w1.numpy())
+    h32 = (acc1.astype(np.float32) * (sx1[:, None] * s1.numpy()[None, :]).astype(np.float32)).astype(np.float32)
+    g32 = F.gelu(torch.from_numpy(h32), approximate="tanh").to(torch.bfloat16)
+    assert not torch.equal(g32, gl)
+
+
+def test_w4a8_linear_and_mlp_composite_step_by_step():
+    """cpu_ref.w4a8_linear / w4a8_mlp = grouped int4 decode to the int8 grid
+    (numpy restatement), then the W8A8 chain with s_channel as the
+    per-channel weight scale."""
+    m, d, f, gs = 64, 256, 512, 128
+    x = outlier_acts(m, d, seed=35, n_out=4)
+    g = torch.Generator().manual_seed(36)
+    w1 = torch.randn(f, d, generator=g) * 0.02
+    w2 = torch.randn(d, f, generator=g) * 0.02
+    p1, r1, c1 = cpu_ref.quantize_w4_weight(w1, gs)
+    p2, r2, c2 = cpu_ref.quantize_w4_weight(w2, gs)
+    w8_1 = npref.w4_decode(p1.numpy(), r1.numpy(), gs)
+    w8_2 = npref.w4_decode(p2.numpy(), r2.numpy(), gs)
+    h = _bf16_chain_linear(bits(x), w8_1, c1.numpy())
+    assert np.array_equal(bits(cpu_ref.w4a8_linear(x, p1, r1, c1, gs)), h)
+    gl = F.gelu(from_bits(h), approximate="tanh")
+    yn = _bf16_chain_linear(bits(gl), w8_2, c2.numpy())
+    assert np.array_equal(bits(cpu_ref.w4a8_mlp(x, p1, r1, c1, p2, r2, c2, gs)), yn)
+    # a decode with swapped nibbles is a different weight grid
+    swapped = ((p1.numpy().view(np.uint8) >> 4) | (p1.numpy().view(np.uint8) << 4)).astype(np.uint8).view(np.int8)
+    assert not np.array_equal(npref.w4_decode(swapped, r1.numpy(), gs), w8_1)
+
+
+def test_int8_linear_gated_residual_composite():
+    """The H3 fc2 boundary without rotation: the int8 projection in the
+    residual's dtype, then residual[t] += y[t] * bf16(gate[row(t)]) with the
+    exact fp32 product and one fp32 and one bf16 rounding of the sum."""
+    m, k, n = 50, 256, 192
+    x = outlier_acts(m, k, seed=37, n_out=4)
+    g = torch.Generator().manual_seed(38)
+    w = torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    sw = _rand_scales(n, 39, 1e-4, 4e-4)
+    res = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    gate = torch.randn(3, n, generator=g) * 0.3
+    segs = ((0, 11, 1), (11, 30, 2), (30, 50, 0))
+    out = cpu_ref.int8_linear_gated_residual_(x, w, sw, None, res.clone(), gate, segs, convrot=False,
+                                              input_act=None)
+    y = from_bits(_bf16_chain_linear(bits(x), w.numpy(), sw.numpy())).double()
+    rows = torch.tensor([r for a, b, r in segs for _ in range(a, b)])
+    want = (res.double() + y * gate.to(torch.bfloat16)[rows].double()).float().to(torch.bfloat16)
+    assert torch.equal(out, want)
+
+
+def test_norm_rope_composite():
+    """cpu_ref.norm_rope = rms_adaln over the whole row, then the split-half
+    rotation per head of head_dim columns: an identity table gives rms_adaln
+    bit for bit; a float64 per-head complex product (heads laid out as
+    consecutive column blocks, pairs (i, i + head_dim/2)) matches within one
+    bf16 rounding; tokens are independent, so swapping two tokens together
+    with their table rows swaps the outputs exactly."""
+    g = torch.Generator().manual_seed(41)
+    m, heads, hd = 6, 5, 128
+    d = heads * hd
+    x = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    sc = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
+    sh = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
+    ident = torch.zeros(1, m, 1, hd // 2, 2, 2)
+    ident[..., 0, 0] = 1
+    ident[..., 1, 1] = 1
+    a = cpu_ref.rms_adaln(x, sc, sh, 1e-6)
+    assert torch.equal(cpu_ref.norm_rope(x, sc, sh, ident, hd, 1e-6), a)
+    ang = torch.rand(m, hd // 2, generator=g) * 6.28
+    c, s = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -s, s, c), -1).reshape(1, m, 1, hd // 2, 2, 2)
+    out = cpu_ref.norm_rope(x, sc, sh, tab, hd, 1e-6).double()
+    ad = a.double()
+    exact = torch.empty(m, d, dtype=torch.float64)
+    for h in range(heads):
+        lo, hi = ad[:, h * hd: h * hd + hd // 2], ad[:, h * hd + hd // 2: (h + 1) * hd]
+        z = torch.complex(lo, hi) * torch.polar(torch.ones_like(ang.double()), ang.double())
+        exact[:, h * hd: h * hd + hd // 2] = z.real
+        exact[:, h * hd + hd // 2: (h + 1) * hd] = z.imag
+    assert ((out - exact).abs() <= 2 ** -8 * exact.abs() + 1e-6).all()
+    perm = torch.tensor([3, 1, 2, 0, 5, 4])
+    out_p = cpu_ref.norm_rope(x[perm], sc, sh, tab[:, perm], hd, 1e-6)
+    assert torch.equal(out_p, cpu_ref.norm_rope(x, sc, sh, tab, hd, 1e-6)[perm])

@@ -124,6 +124,13 @@ struct RowArgs {
   float eps;
 };
 
+// Modulation row of a token under a row map: entries are clamped into the
+// table's mod_rows rows, so a bad map can never read outside the scale/shift
+// tables (callers validate the map; the H3 segment helper does on the host).
+__device__ __forceinline__ int64_t map_row(int32_t r, int64_t mod_rows) {
+  return r < 0 ? 0 : (r >= mod_rows ? mod_rows - 1 : (int64_t)r);
+}
+
 // ---------------------------------------------------------------------------
 // Sum of squares of a row in the reference's reduction order.
 //
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
   }
 
   int64_t mrow = 0;
-  if constexpr (ADALN) mrow = a.row_map ? (int64_t)a.row_map[row] : row / a.mod_group;
+  if constexpr (ADALN) mrow = a.row_map ? map_row(a.row_map[row], a.mod_group) : row / a.mod_group;
   Tab8<TF> tab;
   const int64_t trow = a.freqs_row_stride ? row * a.freqs_row_stride : 0;
   bool tab_loaded = false;
@@ -641,7 +648,7 @@ __global__ __launch_bounds__(512) void adaln_pipe_kernel(RowArgs a, int64_t chun
   const int64_t last = first + chunk < a.rows ? first + chunk : a.rows;
   if (first >= last) return;   // the whole block
   auto mod_row = [&](int64_t row) -> int64_t {
-    return a.row_map ? (int64_t)a.row_map[row] : row / a.mod_group;
+    return a.row_map ? map_row(a.row_map[row], a.mod_group) : row / a.mod_group;
   };
   const int64_t m0 = mod_row(first);
   {
@@ -1196,7 +1203,8 @@ int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D,
   XMH3_REQUIRE(aligned16(x) && aligned16(out) && aligned16(scale) && aligned16(shift) &&
                    (!weight || aligned16(weight)),
                "rms_adaln: pointers must be 16-byte aligned");
-  XMH3_REQUIRE(row_map || mod_group >= 1, "rms_adaln: modulation group must be >= 1");
+  XMH3_REQUIRE(mod_group >= 1, row_map ? "rms_adaln: the modulation table needs >= 1 row"
+                                        : "rms_adaln: modulation group must be >= 1");
   RowArgs a{};
   a.x0 = x; a.o0 = out; a.ldx = ldx; a.ldo = ldo; a.rows = rows; a.D = D; a.weight = weight;
   a.scale = scale; a.shift = shift; a.mod_ld = mod_ld; a.row_map = row_map; a.mod_group = mod_group;

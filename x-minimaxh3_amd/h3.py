@@ -33,10 +33,21 @@ from . import backend, ops
 _ROW_MAPS: dict[tuple, torch.Tensor] = {}
 
 
-def segment_row_map(length: int, segments, device) -> torch.Tensor:
+def segment_row_map(length: int, segments, device, n_rows: int | None = None) -> torch.Tensor:
     """int32 [length]: the modulation row of each token; segments must be an
-    ordered partition ``(start, stop, row)`` of [0, length)."""
-    norm = tuple((int(a), int(b), int(r)) for a, b, r in segments)
+    ordered partition ``(start, stop, row)`` of [0, length). With ``n_rows``
+    (the modulation table's row count) each row is resolved as the
+    reference's ``scale[row]`` indexing resolves it: a negative row counts
+    from the end, a row outside [-n_rows, n_rows) raises IndexError."""
+    norm = []
+    for a, b, r in segments:
+        r = int(r)
+        if n_rows is not None:
+            if not -n_rows <= r < n_rows:
+                raise IndexError(f"index {r} is out of bounds for dimension 0 with size {n_rows}")
+            r = r + n_rows if r < 0 else r
+        norm.append((int(a), int(b), r))
+    norm = tuple(norm)
     dev = torch.device(device)
     key = (dev.type, dev.index, int(length), norm)
     hit = _ROW_MAPS.get(key)
@@ -68,7 +79,9 @@ def rms_adaln(value: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tenso
             raise ValueError("eps is required when norm is a tensor")
     if value.ndim != 2:
         raise ValueError("value must be [tokens, width]")
-    row_map = segment_row_map(value.shape[0], segments, value.device)
+    if scale.ndim != 2 or shift.shape != scale.shape:
+        raise ValueError("scale and shift must be [rows, width] tables of one shape")
+    row_map = segment_row_map(value.shape[0], segments, value.device, n_rows=scale.shape[0])
     return backend.rms_adaln_rows(value, weight, scale.to(value.dtype), shift.to(value.dtype), row_map, eps)
 
 
@@ -127,7 +140,7 @@ def gated_swiglu_mlp_(residual: torch.Tensor, hidden: torch.Tensor, fc1_qweight:
         raise ValueError("MLP chunk_tokens must be positive")
     if hidden.ndim != 2:
         raise ValueError("hidden must be [tokens, width]")
-    rows = segment_row_map(hidden.shape[0], segments, hidden.device)
+    rows = segment_row_map(hidden.shape[0], segments, hidden.device, n_rows=gate.shape[0])
     for start in range(0, hidden.shape[0], chunk_tokens):
         stop = min(start + chunk_tokens, hidden.shape[0])
         raw = ops.int8_linear(hidden[start:stop], fc1_qweight, fc1_scale, fc1_bias, hidden.dtype, convrot=True,

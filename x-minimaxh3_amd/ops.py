@@ -181,9 +181,15 @@ def w4a8_int8_linear(x: torch.Tensor, qdata: torch.Tensor, s_rel: torch.Tensor, 
                      codebook: torch.Tensor | None = None, correction: torch.Tensor | None = None,
                      bias: torch.Tensor | None = None, group_size: int = 16, convrot_groupsize: int = 256,
                      out_dtype: torch.dtype = torch.bfloat16, convrot: bool = True) -> torch.Tensor:
-    """``x @ W.T + bias`` with grouped int4 weights decoded to the int8 grid.
-    ``convrot`` (keyword, default True as in the reference, which always
-    rotates) must be False on this backend."""
+    """``x @ W.T + bias`` with grouped int4 weights decoded to the int8 grid
+    (CK/tensor/w4a8_int8.py:89-115). ``convrot`` is an extra keyword:
+    True (the default, as the reference always rotates) quantizes the
+    activations through the fused ConvRot row quantizer (groups of
+    ``convrot_groupsize`` = 256) against the checkpoint's offline-rotated
+    weights; False selects the unrotated form of the GELU MLP workloads. A
+    ``correction`` adds the asymmetric term of the H3 checkpoints (group sums
+    of the activation codes times the correction, as the reference's GPU
+    dispatcher computes it)."""
     return torch.ops.x_minimaxh3_amd.w4a8_int8_linear(x, qdata, s_rel, s_channel, codebook, correction, bias,
                                                       group_size, convrot_groupsize, DTYPE_TO_CODE[out_dtype],
                                                       convrot)

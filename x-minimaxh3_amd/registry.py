@@ -12,6 +12,7 @@ raises ``NoCapableBackendError`` (there is no silent CPU path).
 from __future__ import annotations
 
 import threading
+from abc import ABC, abstractmethod
 from collections.abc import Callable, Mapping
 from contextlib import contextmanager
 from dataclasses import dataclass, field
@@ -23,6 +24,11 @@ from .exceptions import BackendNotFoundError, BackendNotImplementedError, NoCapa
 
 
 # --------------------------------------------------------------------------- constraints
+# The classes carry every attribute and method the reference's own
+# validation reads (CK/constraints.py:90-255: ``dtypes``, ``devices``,
+# ``shape_rules``, ``check_dtype``, ``check_device``, ``check_shape``,
+# ``default_devices``, ``min_compute_capability``, ``call_rules``), so a
+# capability table built here registers unchanged in the reference registry.
 
 @dataclass(frozen=True)
 class ValidationResult:
@@ -39,8 +45,18 @@ class ValidationResult:
         return ValidationResult(False, param, reason)
 
 
+class ShapeRule(ABC):
+    """A predicate on a tensor's shape with a readable description."""
+
+    @abstractmethod
+    def check(self, t: torch.Tensor) -> bool: ...
+
+    @abstractmethod
+    def describe(self) -> str: ...
+
+
 @dataclass(frozen=True)
-class DivisibleBy:
+class DivisibleBy(ShapeRule):
     dim: int
     factor: int
 
@@ -52,7 +68,7 @@ class DivisibleBy:
 
 
 @dataclass(frozen=True)
-class ExactDims:
+class ExactDims(ShapeRule):
     ndim: int
 
     def check(self, t: torch.Tensor) -> bool:
@@ -63,7 +79,7 @@ class ExactDims:
 
 
 @dataclass(frozen=True)
-class MinDims:
+class MinDims(ShapeRule):
     ndim: int
 
     def check(self, t: torch.Tensor) -> bool:
@@ -75,42 +91,67 @@ class MinDims:
 
 @dataclass(frozen=True)
 class ParamConstraint:
+    """dtypes (None = any; a set of torch dtypes, or Python types for
+    non-tensor arguments), device types (None = the function's default) and
+    shape rules of one argument."""
+
     dtypes: frozenset | None = None
     devices: frozenset[str] | None = None
     shape_rules: tuple = ()
+
+    def check_dtype(self, value: Any) -> bool:
+        if self.dtypes is None:
+            return True
+        dt = value.dtype if isinstance(value, torch.Tensor) else value
+        return dt in self.dtypes or type(value) in self.dtypes
+
+    def check_device(self, tensor: torch.Tensor, default_devices: frozenset[str]) -> bool:
+        allowed = self.devices if self.devices is not None else default_devices
+        return "*" in allowed or tensor.device.type in allowed
+
+    def check_shape(self, tensor: torch.Tensor) -> bool:
+        return all(rule.check(tensor) for rule in self.shape_rules)
 
 
 @dataclass(frozen=True)
 class FunctionConstraints:
     params: dict[str, ParamConstraint] = field(default_factory=dict)
     default_devices: frozenset[str] = frozenset({"cuda"})
+    min_compute_capability: tuple[int, int] | None = None
     call_rules: tuple[Callable[[Mapping[str, Any]], ValidationResult], ...] = ()
 
     def __hash__(self) -> int:
-        return hash((tuple(sorted(self.params)), self.default_devices, self.call_rules))
+        return hash((tuple(sorted(self.params)), self.default_devices, self.min_compute_capability,
+                     self.call_rules))
 
 
-def _check_param(name: str, value: Any, c: ParamConstraint, default_devices: frozenset[str]) -> ValidationResult:
+def validate_param(name: str, value: Any, c: ParamConstraint, default_devices: frozenset[str]) -> ValidationResult:
     if value is None:
         return ValidationResult.ok()
-    if c.dtypes is not None:
+    if not c.check_dtype(value):
         dt = value.dtype if isinstance(value, torch.Tensor) else value
-        if dt not in c.dtypes and type(value) not in c.dtypes:
-            return ValidationResult.fail(name, f"dtype {dt} not in {set(c.dtypes)}")
+        return ValidationResult.fail(name, f"dtype {dt} not in {set(c.dtypes)}")
     if not isinstance(value, torch.Tensor):
         return ValidationResult.ok()
-    devices = c.devices if c.devices is not None else default_devices
-    if "*" not in devices and value.device.type not in devices:
-        return ValidationResult.fail(name, f"device {value.device.type} not in {set(devices)}")
+    if not c.check_device(value, default_devices):
+        allowed = c.devices if c.devices is not None else default_devices
+        return ValidationResult.fail(name, f"device {value.device.type} not in {set(allowed)}")
     for rule in c.shape_rules:
         if not rule.check(value):
             return ValidationResult.fail(name, f"shape {list(value.shape)} fails: {rule.describe()}")
     return ValidationResult.ok()
 
 
-def validate_function_call(c: FunctionConstraints, kwargs: Mapping[str, Any]) -> ValidationResult:
+def validate_function_call(c: FunctionConstraints, kwargs: Mapping[str, Any],
+                           compute_capability: tuple[int, int] | None = None) -> ValidationResult:
+    if c.min_compute_capability is not None:
+        if compute_capability is None:
+            return ValidationResult.fail("__hardware__", "compute capability required but not available")
+        if tuple(compute_capability) < tuple(c.min_compute_capability):
+            return ValidationResult.fail(
+                "__hardware__", f"compute capability {compute_capability} < required {c.min_compute_capability}")
     for name, pc in c.params.items():
-        r = _check_param(name, kwargs.get(name), pc, c.default_devices)
+        r = validate_param(name, kwargs.get(name), pc, c.default_devices)
         if not r.success:
             return r
     for rule in c.call_rules:
@@ -132,6 +173,8 @@ class BackendRegistry:
         self._unavailable: dict[str, str] = {}
         self._lock = threading.Lock()
         self._tls = threading.local()
+        self._cc_known = False
+        self._cc: tuple[int, int] | None = None
 
     # registration ---------------------------------------------------------
     def register(self, name: str, module: Any, capabilities: dict[str, FunctionConstraints]) -> None:
@@ -180,7 +223,19 @@ class BackendRegistry:
         if func not in self._caps.get(backend, ()):
             return ValidationResult.fail("__function__", "not implemented")
         c = self._constraints.get((backend, func))
-        return ValidationResult.ok() if c is None else validate_function_call(c, kwargs)
+        return ValidationResult.ok() if c is None else validate_function_call(c, kwargs, self.compute_capability())
+
+    def compute_capability(self) -> tuple[int, int] | None:
+        """(major, minor) of the current GPU as torch reports it, or None."""
+        if not self._cc_known:
+            self._cc_known = True
+            if torch.cuda.is_available():
+                try:
+                    props = torch.cuda.get_device_properties(torch.cuda.current_device())
+                    self._cc = (props.major, props.minor)
+                except Exception:  # noqa: BLE001 - no device properties: no capability
+                    self._cc = None
+        return self._cc
 
     def get_capable_backend(self, func: str, kwargs: Mapping[str, Any] | None = None) -> str:
         failures: dict[str, str] = {}
