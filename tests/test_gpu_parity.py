@@ -984,3 +984,24 @@ def test_empty_token_batches(pkg, dev):
     # oracle gives no shape here; the fused op returns Q's and K's empty shape
     check((qo, ko), (x, x), "norm_rope")
     torch.cuda.synchronize()
+
+
+def test_host_small_operands_follow_the_input(pkg, dev):
+    """Scales, shifts, norm weights and RoPE tables given on the host are moved
+    to the input's device before the kernels run: the results equal those of
+    the all-device calls bit for bit."""
+    say("host-side small operands")
+    from x_minimaxh3_amd import backend, workloads
+
+    nr = workloads.norm_rope_inputs(grid=(2, 3, 5), d=512, head_dim=128, seed=3)
+    q, k = nr["q"].to(dev), nr["k"].to(dev)
+    want = backend.norm_rope(q, k, nr["scale"].to(dev), nr["shift"].to(dev), nr["freqs"].to(dev), nr["eps"], 128)
+    got = backend.norm_rope(q, k, nr["scale"], nr["shift"], nr["freqs"], nr["eps"], 128)
+    assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+    ra = backend.rms_adaln(q, nr["scale"], nr["shift"])
+    assert torch.equal(ra, backend.rms_adaln(q, nr["scale"].to(dev), nr["shift"].to(dev)))
+    x4 = q.reshape(1, 30, 4, 128)
+    w = (torch.rand(128, generator=torch.Generator().manual_seed(4)) + 0.5).to(torch.bfloat16)
+    a = backend.rms_rope_split_half1(x4, nr["freqs"], w, 1e-6)
+    b = backend.rms_rope_split_half1(x4, nr["freqs"].to(dev), w.to(dev), 1e-6)
+    assert torch.equal(a, b)
