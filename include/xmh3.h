@@ -170,6 +170,21 @@ int xmh3_w8a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, i
                   size_t workspace_bytes, xmh3_stream_t stream);
 
 /*
+ * xmh3_w8a8_mlp without a caller workspace: the workspace is a file-scope
+ * device array of 64 MiB per GPU (held until the process ends), so the call
+ * allocates nothing -- for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Same arguments and results as
+ * xmh3_w8a8_mlp; returns 1 (invalid argument) when
+ * xmh3_w8a8_mlp_workspace_bytes(M, D, F) exceeds 64 MiB (more than 1,439
+ * tokens at d_model 5120, ffn 13824; 3,358 at 1536, 6144). All calls on one GPU share the array:
+ * calls that overlap on one GPU race.
+ */
+int xmh3_w8a8_mlp_noalloc(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                          const int8_t* w1, const float* s1, int s1_per_channel, const int8_t* w2,
+                          const float* s2, int s2_per_channel, void* y, int64_t ldy, xmh3_stream_t stream);
+
+/*
  * The W4A8 MLP block: grouped int4 weights (uniform levels, no rotation),
  * s_rel fp32 or bf16 [N, K/G], per-channel fp32 s_channel.
  * Replaces: the chunked W4A8 MLP (h3serve/native_engine/model/fused_mlp.py:222-266)

@@ -19,6 +19,8 @@
 //   (+ W1 [F,D] i8 | W2 [D,F] i8 for W4A8)
 #include "common.hpp"
 
+#include <mutex>
+
 namespace xmh3 {
 
 int quantize_rows(const void* x, int x_dtype, int input_act, int64_t M, int64_t K, int64_t ldx,
@@ -127,4 +129,64 @@ extern "C" int xmh3_w4a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, i
   if (rc) return rc;
   return mlp_core(x, x_dtype, M, D, F, ldx, ws.w1, w1_schannel, 1, ws.w2, w2_schannel, 1, y, ldy, ws,
                   stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the workspace lives in a file-scope device array
+// instead of a caller buffer, for callers that cannot allocate (code under
+// HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+// Every GPU the library runs on holds its own copy of the array until the
+// process ends; all calls on one GPU share it and it keeps the last call's
+// contents (nothing in it needs to start at zero: each call writes every
+// byte it reads before reading it). Calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+namespace xmh3 {
+
+constexpr size_t kMlpScratchBytes = size_t(64) << 20;   // 64 MiB per GPU
+static __device__ __align__(256) uint8_t scratch[kMlpScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static void* g_scratch_dev[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of this GPU's copy of `scratch` (resolved once per device,
+// with that device current). The array's name is a host-side stand-in, never
+// a device address, so it is only ever used through this pointer.
+static int scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(XMH3_EHIP, "w8a8_mlp_noalloc: no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(XMH3_EHIP, std::string("w8a8_mlp_noalloc: hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return XMH3_OK;
+}
+
+}  // namespace xmh3
+
+extern "C" int xmh3_w8a8_mlp_noalloc(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                                     const int8_t* w1, const float* s1, int s1_per_channel, const int8_t* w2,
+                                     const float* s2, int s2_per_channel, void* y, int64_t ldy,
+                                     hipStream_t stream) {
+  int rc = check_mlp_shapes(M, D, F, ldx, ldy);
+  if (rc) return rc;
+  if (M == 0) return XMH3_OK;
+  const size_t need = carve(nullptr, M, D, F, false).bytes;
+  if (need > kMlpScratchBytes)
+    return fail(XMH3_EINVAL, "w8a8_mlp_noalloc: " + std::to_string(M) + " tokens at d_model " + std::to_string(D) +
+                                 ", ffn " + std::to_string(F) + " need " + std::to_string(need) +
+                                 " bytes of workspace; the static scratch holds " +
+                                 std::to_string(kMlpScratchBytes) + " (use xmh3_w8a8_mlp with a workspace)");
+  XMH3_REQUIRE(x && w1 && s1 && w2 && s2 && y, "w8a8_mlp_noalloc: null pointer");
+  void* base = nullptr;
+  rc = scratch_ptr(&base);
+  if (rc) return rc;
+  const MlpWs ws = carve(base, M, D, F, false);
+  return mlp_core(x, x_dtype, M, D, F, ldx, w1, s1, s1_per_channel, w2, s2, s2_per_channel, y, ldy, ws, stream);
 }
