@@ -185,13 +185,35 @@ int xmh3_w8a8_mlp_noalloc(const void* x, int x_dtype, int64_t M, int64_t D, int6
                           const float* s2, int s2_per_channel, void* y, int64_t ldy, xmh3_stream_t stream);
 
 /*
+ * W4A8 GEMM with the int4 weights unpacked in LDS: out = T(float(acc) *
+ * (sx[m] * s_channel[n])) (+ bias), acc[m, n] = sum_k A[m, k] * w8[n, k],
+ * w8 = clamp(rint((code - 8) * s_rel[n, k/128]), +-127) decoded tile by tile
+ * inside the GEMM (no decoded weight in memory). A: int8 [M, lda];
+ * packed: [N, ldp] bytes (low nibble = even k); s_rel: bf16 or fp32 [N, s_rel_ld]
+ * (s_rel_dtype 2 or 0); group_size 128; K % 256 == 0; bf16 output. Every
+ * weight tile is decoded once per 256-row tile of A, so this form pays off
+ * only where decoding once to memory does not (measured slower than
+ * xmh3_w4_decode_int8 + xmh3_int8_gemm at every M from 256 to 25,200).
+ * Replaces: CK/backends/cuda/ops/w4a8_gemm.cu:123-165 (column-chunked decode
+ * into a scratch buffer feeding the int8 GEMM) and the decode + int8_linear
+ * of CK/backends/eager/w4a8_int8.py:457-508.
+ */
+int xmh3_w4a8_gemm(const int8_t* A, int64_t lda, const uint8_t* packed, int64_t ldp, const void* s_rel,
+                   int s_rel_dtype, int64_t s_rel_ld, int64_t M, int64_t N, int64_t K, int64_t group_size,
+                   const float* sx, const float* s_channel, const void* bias, void* out, int out_dtype,
+                   int64_t ldo, xmh3_stream_t stream);
+
+/*
  * The W4A8 MLP block: grouped int4 weights (uniform levels, no rotation),
- * s_rel fp32 or bf16 [N, K/G], per-channel fp32 s_channel.
+ * s_rel fp32 or bf16 [N, K/G], per-channel fp32 s_channel. Both weights are
+ * decoded once per call to the int8 grid in the workspace (HBM-bound), then
+ * the W8A8 chain runs; group_size is the weights' group (the workspace does
+ * not depend on it).
  * Replaces: the chunked W4A8 MLP (h3serve/native_engine/model/fused_mlp.py:222-266)
  * over w4a8_int8_linear (CK/tensor/w4a8_int8.py:89-115, eager
  * CK/backends/eager/w4a8_int8.py:457-508 decomposed as decode + int8_linear).
  */
-size_t xmh3_w4a8_mlp_workspace_bytes(int64_t M, int64_t D, int64_t F);
+size_t xmh3_w4a8_mlp_workspace_bytes(int64_t M, int64_t D, int64_t F, int64_t group_size);
 int xmh3_w4a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
                   const uint8_t* w1_packed, const void* w1_srel, const float* w1_schannel,
                   const uint8_t* w2_packed, const void* w2_srel, const float* w2_schannel,

@@ -52,7 +52,9 @@ def test_workspace_queries_without_gpu(pkg):
     for b in (25200 * 5120, 25200 * 4, 25200 * 13824 * 2, 25200 * 4, 25200 * 13824, 25200 * 4):
         expect += (b + 255) // 256 * 256
     assert n == expect
-    assert lib.xmh3_w4a8_mlp_workspace_bytes(64, 256, 512) > lib.xmh3_w8a8_mlp_workspace_bytes(64, 256, 512)
+    # the W8A8 regions plus both weights decoded to the int8 grid
+    w4 = lib.xmh3_w4a8_mlp_workspace_bytes(25200, 5120, 13824, 128)
+    assert w4 == n + (13824 * 5120 + 255) // 256 * 256 * 2
 
 
 def test_argument_errors_need_no_gpu(pkg):

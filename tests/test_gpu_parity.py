@@ -355,6 +355,49 @@ def test_w4a8_linear_and_mlp(pkg, dev):
     close(ym, ymr, "w4a8 mlp")
 
 
+@pytest.mark.parametrize("m,n,k,srel_dtype,srel_pad,bias", [
+    (777, 1000, 768, torch.bfloat16, 1, False),
+    (300, 512, 1024, torch.float32, 0, True),
+    (256, 256, 256, torch.bfloat16, 0, False),
+    (1030, 2304, 5120, torch.bfloat16, 3, True),
+])
+def test_w4a8_gemm_lds_decode(pkg, dev, m, n, k, srel_dtype, srel_pad, bias):
+    """xmh3_w4a8_gemm (int4 codes unpacked in LDS inside the GEMM, group 128)
+    against the oracle's decode + int8 linear, bit for bit: ragged M and N,
+    bf16 / fp32 s_rel, s_rel rows padded to an odd stride (bf16 values in both
+    halves of their dwords), optional bias."""
+    say(f"w4a8 gemm lds decode m={m} n={n} k={k} s_rel={srel_dtype} pad={srel_pad} bias={bias}")
+    from x_minimaxh3_amd import _lib, workloads
+
+    g = torch.Generator().manual_seed(m + n)
+    x = outlier_acts(m, k, seed=n)
+    w = torch.randn(n, k, generator=g) * 0.02
+    packed, srel, sch = workloads.quantize_weight_w4(w, 128, srel_dtype)
+    wide = torch.zeros(n, k // 128 + srel_pad, dtype=srel_dtype)
+    wide[:, : k // 128] = srel
+    srel_v = wide.to(dev)[:, : k // 128]                      # row stride k/128 + pad
+    b = (torch.randn(n, generator=g) * 0.1).to(torch.bfloat16) if bias else None
+    q, xs = cpu_ref.quantize_int8_rowwise(x)
+    qd, xsd = q.to(dev), xs.to(dev)
+    pd, schd = packed.to(dev), sch.to(dev)
+    bd = None if b is None else b.to(dev)
+    out = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+    rc = _lib.load().xmh3_w4a8_gemm(qd.data_ptr(), k, pd.data_ptr(), k // 2, srel_v.data_ptr(),
+                                    _lib.DTYPE_CODE[srel_dtype], srel_v.stride(0), m, n, k, 128, xsd.data_ptr(),
+                                    schd.data_ptr(), None if bd is None else bd.data_ptr(), out.data_ptr(), 2, n,
+                                    _lib.stream_of(qd))
+    assert rc == 0, _lib.load().xmh3_last_error()
+    torch.cuda.synchronize()
+    want = cpu_ref.w4a8_linear(x, packed, srel.float(), sch, 128, bias=b)
+    assert same(out, want, "w4a8 gemm")
+    if not srel_pad:
+        # the torch-facing wrapper and the decode-once linear agree with it
+        from x_minimaxh3_amd import backend
+        got = backend.w4a8_linear_lds_decode(x.to(dev), pd, srel.to(dev), schd, bd)
+        ref = pkg.w4a8_int8_linear(x.to(dev), pd, srel.to(dev), schd, bias=bd, group_size=128, convrot=False)
+        assert same(got, want, "lds-decode wrapper") and same(ref, want, "decode-once linear")
+
+
 def test_w4a8_mlp_720p_row_sample(pkg, dev):
     """C4 at its full shape: 25,200 tokens, 5120 -> 13824 -> 5120, int4 group
     128 (40 groups along fc1's K, 108 along fc2's), bf16 s_rel. Both linears

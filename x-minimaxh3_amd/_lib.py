@@ -49,7 +49,9 @@ SIGNATURES: dict[str, tuple] = {
                               c_void_p, c_int, c_void_p, c_i64, c_void_p, c_size, c_void_p]),
     "xmh3_w8a8_mlp_noalloc": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_int,
                                       c_void_p, c_void_p, c_int, c_void_p, c_i64, c_void_p]),
-    "xmh3_w4a8_mlp_workspace_bytes": (c_size, [c_i64, c_i64, c_i64]),
+    "xmh3_w4a8_mlp_workspace_bytes": (c_size, [c_i64, c_i64, c_i64, c_i64]),
+    "xmh3_w4a8_gemm": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, c_i64,
+                               c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_i64, c_void_p]),
     "xmh3_w4a8_mlp": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_void_p, c_void_p, c_int, c_i64, c_void_p, c_i64, c_void_p, c_size,
                               c_void_p]),

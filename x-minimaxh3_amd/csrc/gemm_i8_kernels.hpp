@@ -29,6 +29,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "w4_lut.hpp"
 
 #include <type_traits>
 #include <utility>
@@ -71,6 +72,12 @@ struct GemmArgs {
   const int32_t* gate_rows;    // [M], clamped into [0, gate_nrows)
   int gate_nrows;
   int row_stores;              // dequant epilogue may store whole rows (N, ldo % 8 == 0, out 16-B aligned)
+  // W4 weights (gemm_i8_pp_kernel<..., true>): B is the packed int4 [N, K/2]
+  // (row stride ldb bytes) decoded in LDS with s_rel [N, K/128] (row stride
+  // srel_ld elements, bf16 or fp32); sw is s_channel
+  const void* srel;
+  int64_t srel_ld;
+  int srel_bf16;
 };
 
 #ifndef XMH3_GROUP_M
@@ -569,7 +576,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
 // sub-tile (rows 128*(w&1), columns 64*(w>>1)): 8 x 4 accumulators of
 // v_mfma_i32_16x16x64_i8 in 128 AGPRs, 96 VGPRs of fragments.
 //
-// LDS (160 KiB): the B tile (weights, 256 rows x 128 bytes = 32 KiB per
+// LDS (160 KiB). int8 weights: the B tile (256 rows x 128 bytes = 32 KiB per
 // K-step) in a ring of three buffers at [0, 96K), the A tile in two buffers
 // at [96K, 160K). A 16-byte chunk c of row r sits at slot c ^ (r & 7)
 // (conflict-free ds_read_b128). The DMA is buffer_load_dwordx4 ... lds, 8
@@ -586,14 +593,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm_i8_dma_kernel(GemmArgs p) {
 // so each memory phase carries 8 DMA and 24 fragment reads per wave, A
 // slices are issued two phases and B slices three phases before they are
 // read.
+//
+// W4 weights (group 128 = one K-step): the B ring holds the decoded int8
+// tile in two buffers at [0, 64K) and A is at [64K, 128K). Wave w owns B rows
+// 32w .. 32w+31: their packed int4 slice (64 bytes per row and step) and
+// s_rel dwords are staged by DMA in the wave's own part of [128K, 146K). In
+// its memory phase of step t the wave first decodes slice t+1 through the
+// rows' 16-entry level tables (w4_lut.hpp) into the int8 B buffer (t+1)&1
+// (P's half in phase 2t, Q's in 2t+1, both before the barrier that opens P's
+// reads of step t+1), then stages slice t+2 in the buffer it has just read
+// and issues its A refill. Decoding before issuing keeps the only DMA still
+// in flight at the decode the one it waits for. The MFMA side and the
+// epilogue are those of int8 weights, with s_channel as the per-channel
+// scale.
 // ---------------------------------------------------------------------------
 constexpr int PP_BK = 128;                 // K bytes per step
 constexpr int PP_THREADS = 512;
 constexpr int PP_TILE = BM * PP_BK;        // 32 KiB: one operand tile of one step
-constexpr int PP_A0 = 3 * PP_TILE;         // A ring after the three B buffers
 constexpr int PP_LDS = 5 * PP_TILE;        // 160 KiB
 constexpr int PP_TAIL = 4;                 // MFMAs of P's phase issued after its barrier
 constexpr int PP_SLICE = 16 * 144;         // per-wave epilogue transpose slice
+constexpr int PP_W4_PK0 = 4 * PP_TILE;     // W4: packed B slice staging (16 KiB)
+constexpr int PP_W4_SR0 = PP_W4_PK0 + BN * PP_BK / 2;   // W4: s_rel staging (256 bytes per wave)
+template <bool W4>
+constexpr int pp_a0() { return W4 ? 2 * PP_TILE : 3 * PP_TILE; }   // A ring
 
 // Raw buffer resource over [base, base + bytes): word 3 is the gfx9 data format
 // for untyped dword access.
@@ -665,9 +688,10 @@ __device__ __forceinline__ void epilogue_rows_lds(const GemmArgs& p, v4i (&acc)[
   });
 }
 
-template <int EPI, typename TO, bool VEC_OUT>
+template <int EPI, typename TO, bool VEC_OUT, bool W4>
 __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) int8_t lds[PP_LDS];
+  constexpr int A0 = pp_a0<W4>();
 
   int tm, tn;
   tile_coords(blockIdx.x, p.tiles_m, p.tiles_n, tm, tn);
@@ -678,11 +702,13 @@ __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
   const bool grp_p = wave < 4;
   const int rows_a = min(BM, p.M - m0), rows_b = min(BN, p.N - n0);
   const int lda = (int)p.lda, ldb = (int)p.ldb;
-  // P waves DMA the A tile, Q waves the B tile: rows 64*dw .. 64*dw + 63
+  // int8 weights: P waves DMA the A tile, Q waves the B tile, rows
+  // 64*dw .. 64*dw + 63. W4: P waves DMA A, every wave its packed B rows.
   const int dw = wave & 3;
-  const __amdgpu_buffer_rsrc_t rsrc = grp_p ? raw_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)(rows_a * lda))
-                                            : raw_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)(rows_b * ldb));
-  const uint32_t lim = (uint32_t)((grp_p ? rows_a : rows_b) - 1), ld = (uint32_t)(grp_p ? lda : ldb);
+  const __amdgpu_buffer_rsrc_t rsrc = (grp_p || W4) ? raw_rsrc(p.A + (int64_t)m0 * p.lda, (uint32_t)(rows_a * lda))
+                                                    : raw_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)(rows_b * ldb));
+  const uint32_t lim = (uint32_t)(((grp_p || W4) ? rows_a : rows_b) - 1);
+  const uint32_t ld = (uint32_t)((grp_p || W4) ? lda : ldb);
   // lane l of DMA instruction g fetches row r0 + 8g (clamped), 16-byte chunk
   // (l & 7) ^ (row & 7), landing at byte 16 l of the instruction's 1 KiB
   const int r0 = dw * 64 + (lane >> 3);
@@ -706,12 +732,74 @@ __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
     });
   };
 
+  // W4: wave w's packed rows 32w .. 32w+31 (64 bytes each per step), two DMA
+  // of 16 rows, and one dword DMA of the rows' s_rel (lane l: row 32w + l;
+  // a bf16 value is read in its 4-byte aligned dword, which lies in the same
+  // page as the value). The decoding lane's row is 32w + lane/2, its half of
+  // the row's 128 codes lane & 1.
+  const int w4_row = 32 * wave + (lane >> 1), w4_half = lane & 1;
+  __amdgpu_buffer_rsrc_t rsrc_w4, rsrc_sr;
+  uint32_t pk_off[2] = {0, 0}, sr_off = 0;
+  int sr_esize = 4;
+  if constexpr (W4) {
+    rsrc_w4 = raw_rsrc(p.B + (int64_t)n0 * p.ldb, (uint32_t)(rows_b * ldb));
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int r = 32 * wave + 16 * g + (lane >> 2);
+      pk_off[g] = (uint32_t)(min(r, rows_b - 1) * ldb + (lane & 3) * 16);
+    }
+    sr_esize = p.srel_bf16 ? 2 : 4;
+    // based at s_rel itself (4-byte aligned, host-checked) so that each
+    // dword offset below is 4-byte aligned in memory
+    const uint32_t sr_bytes = (uint32_t)(((int64_t)(n0 + rows_b) * p.srel_ld * sr_esize + 3) & ~3LL);
+    rsrc_sr = raw_rsrc(p.srel, sr_bytes);
+    sr_off = (uint32_t)((int64_t)(n0 + min(32 * wave + lane, rows_b - 1)) * p.srel_ld * sr_esize);
+  }
+  auto issue_w4 = [&](int kslice) __attribute__((always_inline)) {
+    int8_t* base = lds + PP_W4_PK0 + wave * 2048;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_w4, (lds_void_t*)(base + g * 1024), 16, pk_off[g],
+                                               kslice * (PP_BK / 2), 0, 0);
+    const uint32_t e = sr_off + (uint32_t)(kslice * sr_esize);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc_sr, (lds_void_t*)(lds + PP_W4_SR0 + wave * 256), 4, e & ~3u, 0, 0,
+                                             0);
+  };
+  // decode this lane's 64 codes of the staged slice kslice into B buffer bbuf
+  auto decode_w4 = [&](int kslice, int bbuf) __attribute__((always_inline)) {
+    const int8_t* src = lds + PP_W4_PK0 + wave * 2048 + (lane >> 1) * 64 + w4_half * 32;
+    const uint4 p0 = *reinterpret_cast<const uint4*>(src);
+    const uint4 p1 = *reinterpret_cast<const uint4*>(src + 16);
+    const uint32_t sw = *reinterpret_cast<const uint32_t*>(lds + PP_W4_SR0 + wave * 256 + (lane >> 1) * 4);
+    float s;
+    if (p.srel_bf16) {
+      // the value sits in the upper half of its dword when its element index is odd
+      const bool upper = (((int64_t)(n0 + min(w4_row, rows_b - 1)) * p.srel_ld + kslice) & 1) != 0;
+      s = bf16_to_f32(upper ? (sw >> 16) : (sw & 0xffffu));
+    } else {
+      s = __uint_as_float(sw);
+    }
+    uint32_t lut[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      lut[w] = w4_entry4((float)(4 * w - 8), (float)(4 * w - 7), (float)(4 * w - 6), (float)(4 * w - 5), s);
+    const uint32_t pw[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+    int8_t* dst = lds + bbuf * PP_TILE + w4_row * PP_BK;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint4 o = make_uint4(w4_lookup4<0x01010000u>(pw[2 * c], lut), w4_lookup4<0x03030202u>(pw[2 * c], lut),
+                                 w4_lookup4<0x01010000u>(pw[2 * c + 1], lut),
+                                 w4_lookup4<0x03030202u>(pw[2 * c + 1], lut));
+      *reinterpret_cast<uint4*>(dst + (((4 * w4_half + c) ^ (w4_row & 7)) * 16)) = o;
+    }
+  };
+
   v4i acc[8][4];
   static_for<8>([&](auto I) { static_for<4>([&](auto J) { acc[I][J] = v4i{0, 0, 0, 0}; }); });
 
   // fragment (i or j, half h): row base + lane%16, logical chunk 4h + lane/16
   const int frow = lane & 15, fchunk = lane >> 4;
-  const int fa_off = PP_A0 + (wm * 128 + frow) * PP_BK;
+  const int fa_off = A0 + (wm * 128 + frow) * PP_BK;
   const int fb_off = (wn * 64 + frow) * PP_BK;
   const int sw0 = ((fchunk) ^ (frow & 7)) * 16, sw1 = ((4 + fchunk) ^ (frow & 7)) * 16;
   v4i fa[2][8], fb[2][4];
@@ -747,7 +835,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
             v4i& c = acc[I][J];
             const v4i& xb = fb[H][J];
             const v4i& xa = fa[H][I];
-            const int lst = last;
+            const int lst = __builtin_amdgcn_readfirstlane(last);   // an SGPR operand in every variant
             if constexpr (idx == 63)
               asm volatile(
                   "v_mfma_i32_16x16x64_i8 %0, %1, %2, %0\n\t"
@@ -770,23 +858,42 @@ __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
   using M64 = std::integral_constant<int, 64>;
   const int ksteps = p.K / PP_BK;  // even, >= 2 (host: K % 256 == 0)
 
+  // W4 prologue (every wave; P also its A slice 0): stage and decode slice 0
+  // into B buffer 0, then stage slice 1.
+  if constexpr (W4) {
+    if (grp_p) issue(0, A0);
+    issue_w4(0);
+    wait_vmcnt<0>();
+    decode_w4(0, 0);
+    wait_lgkm0();
+    issue_w4(min(1, ksteps - 1));
+  }
+
   // Past the end the DMA re-fetches the last slice into buffers nobody reads
   // any more; everything stays in bounds.
   if (grp_p) {
-    issue(0, PP_A0);
-    wait_vmcnt<0>();
+    if constexpr (!W4) {
+      issue(0, A0);
+      wait_vmcnt<0>();
+    }
     s_barrier();
     int bbuf = 0;
     auto step = [&](int t, auto ASTG) __attribute__((always_inline)) {
       constexpr int sa = decltype(ASTG)::value;
       const int last = __builtin_amdgcn_readfirstlane(t + 1 == ksteps);
-      issue(min(t + 1, ksteps - 1), PP_A0 + (sa ^ 1) * PP_TILE);
-      load_frags(ASTG, bbuf);
-      bbuf = bbuf == 2 ? 0 : bbuf + 1;
+      if constexpr (W4) {
+        wait_vmcnt<0>();         // staged slice t+1 (already landed from step 1 on)
+        decode_w4(min(t + 1, ksteps - 1), sa ^ 1);
+        wait_lgkm0();
+        issue_w4(min(t + 2, ksteps - 1));
+      }
+      issue(min(t + 1, ksteps - 1), A0 + (sa ^ 1) * PP_TILE);
+      load_frags(ASTG, W4 ? sa : bbuf);
+      if constexpr (!W4) bbuf = bbuf == 2 ? 0 : bbuf + 1;
       wait_lgkm0();
       s_barrier();
       mfmas(last, M0{}, MT{});
-      wait_vmcnt<0>();
+      wait_vmcnt<0>();           // A slice t+1 landed (W4: and the staged slice t+2)
       s_barrier();
       mfmas(last, MT{}, M64{});
     };
@@ -795,21 +902,33 @@ __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
       step(t + 1, C1{});
     }
   } else {
-    issue(0, 0);
-    issue(min(1, ksteps - 1), PP_TILE);
-    wait_vmcnt<0>();
+    if constexpr (!W4) {
+      issue(0, 0);
+      issue(min(1, ksteps - 1), PP_TILE);
+      wait_vmcnt<0>();
+    }
     s_barrier();
     int bbuf = 0, bnext = 2;
     // the barrier opening step t closes Q's MFMA phase of step t-1 (for
     // t = 0: P's first memory phase)
     auto step = [&](int t, auto ASTG) __attribute__((always_inline)) {
+      constexpr int sa = decltype(ASTG)::value;
       s_barrier();
-      issue(min(t + 2, ksteps - 1), bnext * PP_TILE);
-      bnext = bnext == 2 ? 0 : bnext + 1;
-      load_frags(ASTG, bbuf);
-      bbuf = bbuf == 2 ? 0 : bbuf + 1;
-      wait_lgkm0();
-      wait_vmcnt<8>();  // slice t+1 landed; the 8 DMA of slice t+2 may stay in flight
+      if constexpr (W4) {
+        wait_vmcnt<0>();         // staged slice t+1 landed
+        decode_w4(min(t + 1, ksteps - 1), sa ^ 1);
+        wait_lgkm0();
+        issue_w4(min(t + 2, ksteps - 1));
+        load_frags(ASTG, sa);
+        wait_lgkm0();
+      } else {
+        issue(min(t + 2, ksteps - 1), bnext * PP_TILE);
+        bnext = bnext == 2 ? 0 : bnext + 1;
+        load_frags(ASTG, bbuf);
+        bbuf = bbuf == 2 ? 0 : bbuf + 1;
+        wait_lgkm0();
+        wait_vmcnt<8>();         // slice t+1 landed; the 8 DMA of slice t+2 may stay in flight
+      }
       s_barrier();
       mfmas(__builtin_amdgcn_readfirstlane(t + 1 == ksteps), M0{}, M64{});
     };
@@ -824,10 +943,10 @@ __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
   load_scales_t<EPI, 8, 4>(p, row0, col0, lane, sc);
   // The A ring is idle once P has passed its last barrier (every A DMA has
   // landed and Q's last reads of it are done), so each wave's transpose slice
-  // lives there; Q's last B refill may still be landing in the B ring.
+  // lives there; the last refills of the other rings may still be landing.
   if constexpr (EPI == EPI_DEQUANT && !std::is_same<TO, F32T>::value) {
     if (p.row_stores) {
-      int8_t* slice = lds + PP_A0 + wave * PP_SLICE;
+      int8_t* slice = lds + A0 + wave * PP_SLICE;
       if (p.bias)
         epilogue_rows_lds<TO, true>(p, acc, sc, row0, col0, lane, slice);
       else
@@ -852,9 +971,9 @@ inline int launch_gemm_T(GemmArgs& a, bool vec, hipStream_t st) {
   constexpr bool only_vec = EPI == EPI_GATED;
   if (a.K % (2 * PP_BK) == 0 && spans_ok) {
     if (vec || only_vec)
-      hipLaunchKernelGGL((gemm_i8_pp_kernel<EPI, TO, true>), grid, dim3(PP_THREADS), 0, st, a);
+      hipLaunchKernelGGL((gemm_i8_pp_kernel<EPI, TO, true, false>), grid, dim3(PP_THREADS), 0, st, a);
     else if constexpr (!only_vec)
-      hipLaunchKernelGGL((gemm_i8_pp_kernel<EPI, TO, false>), grid, dim3(PP_THREADS), 0, st, a);
+      hipLaunchKernelGGL((gemm_i8_pp_kernel<EPI, TO, false, false>), grid, dim3(PP_THREADS), 0, st, a);
     return check_launch("gemm_i8_pp_kernel");
   }
   if (a.K % (2 * DMA_BK) == 0 && spans_ok) {
@@ -873,6 +992,14 @@ inline int launch_gemm_T(GemmArgs& a, bool vec, hipStream_t st) {
 
 template <int EPI, typename TO>
 int launch_gemm(GemmArgs& a, bool vec, hipStream_t st);
+
+// W4 weights: K % 256 == 0, group 128, operand spans < 2^31 (host checks)
+template <int EPI, typename TO>
+inline int launch_gemm_w4_T(GemmArgs& a, hipStream_t st) {
+  dim3 grid((unsigned)(a.tiles_m * a.tiles_n));
+  hipLaunchKernelGGL((gemm_i8_pp_kernel<EPI, TO, true, true>), grid, dim3(PP_THREADS), 0, st, a);
+  return check_launch("gemm_i8_pp_kernel (W4)");
+}
 
 #define XMH3_INSTANTIATE_GEMM(EPI, TO)                                      \
   template <>                                                             \
