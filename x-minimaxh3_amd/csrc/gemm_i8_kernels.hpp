@@ -29,6 +29,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "tile_map.hpp"
 #include "w4_lut.hpp"
 
 #include <type_traits>
@@ -80,38 +81,13 @@ struct GemmArgs {
   int srel_bf16;
 };
 
-#ifndef XMH3_GROUP_M
-#define XMH3_GROUP_M 4
-#endif
-#ifndef XMH3_NUM_XCD
-#define XMH3_NUM_XCD 8
-#endif
 constexpr int BM = 256, BN = 256, NTHREADS = 256;
-constexpr int GROUP_M = XMH3_GROUP_M;   // M-tiles per swizzle group
-constexpr int NUM_XCD = XMH3_NUM_XCD;   // XCDs workgroups are dealt over
 
 // XOR swizzle of the 16-byte chunk index inside an LDS row of BK bytes.
 template <int BK>
 __device__ __forceinline__ int swz(int row, int chunk) {
   if constexpr (BK == 64) return chunk ^ ((row >> 1) & 3);
   else return chunk ^ (row & 7);
-}
-
-// Map the hardware workgroup id to (tile_m, tile_n): contiguous logical tile
-// ranges per XCD (workgroups are dealt round-robin over the XCDs), then a
-// GROUP_M swizzle inside the logical order.
-__device__ __forceinline__ void tile_coords(int pid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  const int q = total / NUM_XCD, r = total % NUM_XCD;
-  const int x = pid % NUM_XCD, j = pid / NUM_XCD;
-  const int logical = (x < r) ? x * (q + 1) + j : r * (q + 1) + (x - r) * q + j;
-  const int in_group = GROUP_M * tiles_n;
-  const int group = logical / in_group;
-  const int first_m = group * GROUP_M;
-  const int gsize = min(tiles_m - first_m, GROUP_M);
-  const int rem = logical - group * in_group;
-  tm = first_m + rem % gsize;
-  tn = rem / gsize;
 }
 
 // 4 consecutive outputs -> one 8- or 16-byte store
@@ -135,12 +111,70 @@ __device__ __forceinline__ void store4(float* p, const float* v, F32T) {
 // in registers. The row and column scales of the sub-tile are all loaded in
 // one batch when the main loop ends (the fragment registers are free then), so
 // the epilogue pays one memory latency instead of one per output element.
+//
+// An epilogue reads its scales through a scale source: row(i) is the row
+// scale of row em + 16 i, col4(j, w) the column scales of columns
+// en + 16 j + {0..3}, bias4<TO>(p, n, j, b) the bias there as a float (value
+// in TO); em = row0 + lane % 16 and en = col0 + 4 (lane / 16).
 template <int NI = 8, int NJ = 8>
 struct EpiScalesT {
   float sx[NI];      // rows m = em + 16 i
   float sw[NJ][4];   // columns n = en + 16 j + r
+  __device__ __forceinline__ float row(int i) const { return sx[i]; }
+  __device__ __forceinline__ void col4(int j, float (&w)[4]) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) w[r] = sw[j][r];
+  }
+  template <typename TO>
+  __device__ __forceinline__ void bias4(const GemmArgs& p, int n, int, float (&b)[4]) const {
+    const typename TO::storage* brow = static_cast<const typename TO::storage*>(p.bias);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) b[r] = TO::load(brow[min(n + r, p.N - 1)]);
+  }
 };
 using EpiScales = EpiScalesT<8, 8>;
+
+// The same scales staged once per wave in LDS (the ping-pong kernel, whose
+// 128 VGPRs per lane cannot also hold 24 scales and 16 bias values through
+// the epilogue): [128] row scales | [64] column scales | [64] bias (float),
+// one 1 KiB region per wave, written and read by that wave only.
+struct LdsScales {
+  const float* base;
+  int m16, c4;
+  __device__ __forceinline__ float row(int i) const { return base[16 * i + m16]; }
+  __device__ __forceinline__ void col4(int j, float (&w)[4]) const {
+    const float4 v = *reinterpret_cast<const float4*>(base + 128 + 16 * j + c4);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  }
+  template <typename TO>
+  __device__ __forceinline__ void bias4(const GemmArgs&, int, int j, float (&b)[4]) const {
+    const float4 v = *reinterpret_cast<const float4*>(base + 192 + 16 * j + c4);
+    b[0] = v.x; b[1] = v.y; b[2] = v.z; b[3] = v.w;
+  }
+};
+constexpr int LDS_SCALES_BYTES = 1024;
+
+// Stage a 128 x 64 wave sub-tile's scales (and bias) at dst: four loads per
+// lane (indices clamped into range; rows and columns past the end are never
+// stored) in place of 24 (+16) per lane.
+template <int EPI, typename TO>
+__device__ __forceinline__ LdsScales stage_scales(const GemmArgs& p, int row0, int col0, int lane, float* dst) {
+  if constexpr (EPI != EPI_INT32) {
+    const float a = p.sx[min(row0 + lane, p.M - 1)];
+    const float b = p.sx[min(row0 + 64 + lane, p.M - 1)];
+    const float w = p.sw[p.sw_per_channel ? min(col0 + lane, p.N - 1) : 0];
+    float bv = 0.0f;
+    if (p.bias) bv = TO::load(static_cast<const typename TO::storage*>(p.bias)[min(col0 + lane, p.N - 1)]);
+    dst[lane] = a;
+    dst[64 + lane] = b;
+    dst[128 + lane] = w;
+    dst[192 + lane] = bv;
+  }
+  // a wave's LDS operations execute in order; the reads of other lanes'
+  // values must stay below these writes
+  asm volatile("" ::: "memory");
+  return LdsScales{dst, lane & 15, 4 * (lane >> 4)};
+}
 
 // (row0, col0): origin of the wave's NI*16 x NJ*16 sub-tile
 template <int EPI, int NI, int NJ>
@@ -168,8 +202,8 @@ __device__ __forceinline__ void load_scales(const GemmArgs& p, int m0, int n0, i
   load_scales_t<EPI, 8, 8>(p, m0 + wm * 128, n0 + wn * 128, lane, sc);
 }
 
-template <int EPI, typename TO, bool VEC_OUT, bool BIAS, int NI, int NJ>
-__device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][NJ], const EpiScalesT<NI, NJ>& sc,
+template <int EPI, typename TO, bool VEC_OUT, bool BIAS, int NI, int NJ, typename SC>
+__device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][NJ], const SC& sc,
                                               int row0, int col0, int lane) {
   const int em = row0 + (lane & 15);
   const int en = col0 + 4 * (lane >> 4);
@@ -179,7 +213,7 @@ __device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][
     const bool mok = m < p.M;
     float amax = 0.0f;
     float sxm = 0.0f;
-    if constexpr (EPI != EPI_INT32) sxm = sc.sx[i];
+    if constexpr (EPI != EPI_INT32) sxm = sc.row(i);
     static_for<NJ>([&](auto J) {
       constexpr int j = J;
       const int n = en + j * 16;
@@ -196,16 +230,17 @@ __device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][
         }
       } else {
         typename TO::storage* orow = static_cast<typename TO::storage*>(p.out) + (int64_t)m * p.ldo;
-        const typename TO::storage* brow = static_cast<const typename TO::storage*>(p.bias);
-        float v[4];
+        float v[4], w[4], bv[4];
+        sc.col4(j, w);
+        if constexpr (BIAS) sc.template bias4<TO>(p, n, j, bv);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool nok = n + r < p.N;
-          float y = (float)acc[i][j][r] * (sxm * sc.sw[j][r]);
+          float y = (float)acc[i][j][r] * (sxm * w[r]);
           // the stores round to TO once; the bias add and GELU need the value
           // in TO first (the reference materialises it there)
           if constexpr (BIAS || EPI == EPI_GELU) y = TO::round(y);
-          if constexpr (BIAS) y = TO::round(y + TO::load(brow[min(n + r, p.N - 1)]));
+          if constexpr (BIAS) y = TO::round(y + bv[r]);
           if constexpr (EPI == EPI_GELU) {
             y = TO::round(gelu_tanh_f32(y));
             amax = fmaxf(amax, nok ? fabsf(y) : 0.0f);
@@ -239,14 +274,13 @@ __device__ __forceinline__ void epilogue_body(const GemmArgs& p, v4i (&acc)[NI][
 // and gate rows 8- (16- for an fp32 gate) byte aligned, so every column block
 // of 4 is one vector load; rows and columns past the end are clamped for the
 // loads and not stored.
-template <typename TO, bool BIAS, int NI, int NJ>
-__device__ __forceinline__ void epilogue_gated(const GemmArgs& p, v4i (&acc)[NI][NJ], const EpiScalesT<NI, NJ>& sc,
+template <typename TO, bool BIAS, int NI, int NJ, typename SC>
+__device__ __forceinline__ void epilogue_gated(const GemmArgs& p, v4i (&acc)[NI][NJ], const SC& sc,
                                                int row0, int col0, int lane) {
   using S = typename TO::storage;
   const int em = row0 + (lane & 15);
   const int en = col0 + 4 * (lane >> 4);
   S* const res_base = static_cast<S*>(p.out);
-  const S* const brow = static_cast<const S*>(p.bias);
   uint2 res[2][NJ];
   float gt[2][NJ][4];
   auto fetch = [&](auto I) __attribute__((always_inline)) {
@@ -274,17 +308,19 @@ __device__ __forceinline__ void epilogue_gated(const GemmArgs& p, v4i (&acc)[NI]
     if constexpr (i + 1 < NI) fetch(std::integral_constant<int, i + 1>{});
     const int m = em + i * 16;
     const bool mok = m < p.M;
-    const float sxm = sc.sx[i];
+    const float sxm = sc.row(i);
     S* orow = res_base + (int64_t)m * p.ldo;
     static_for<NJ>([&](auto J) {
       constexpr int j = J;
       const int n = en + j * 16;
       const uint32_t rw[2] = {res[b][j].x, res[b][j].y};
-      float v[4];
+      float v[4], w[4], bv[4];
+      sc.col4(j, w);
+      if constexpr (BIAS) sc.template bias4<TO>(p, n, j, bv);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float y = TO::round((float)acc[i][j][r] * (sxm * sc.sw[j][r]));
-        if constexpr (BIAS) y = TO::round(y + TO::load(brow[min(n + r, p.N - 1)]));
+        float y = TO::round((float)acc[i][j][r] * (sxm * w[r]));
+        if constexpr (BIAS) y = TO::round(y + bv[r]);
         const float g = TO::round(gt[b][j][r]);
         const float rv = TO::load((rw[r >> 1] >> (16 * (r & 1))) & 0xffffu);
         v[r] = TO::round(rv + y * g);
@@ -296,19 +332,19 @@ __device__ __forceinline__ void epilogue_gated(const GemmArgs& p, v4i (&acc)[NI]
 
 // The bias test is hoisted out of the element loop (a uniform branch per
 // element otherwise).
-template <int EPI, typename TO, bool VEC_OUT, int NI, int NJ>
-__device__ __forceinline__ void epilogue_t(const GemmArgs& p, v4i (&acc)[NI][NJ], const EpiScalesT<NI, NJ>& sc,
+template <int EPI, typename TO, bool VEC_OUT, int NI, int NJ, typename SC>
+__device__ __forceinline__ void epilogue_t(const GemmArgs& p, v4i (&acc)[NI][NJ], const SC& sc,
                                            int row0, int col0, int lane) {
   if constexpr (EPI == EPI_GATED) {
     if (p.bias)
-      epilogue_gated<TO, true, NI, NJ>(p, acc, sc, row0, col0, lane);
+      epilogue_gated<TO, true>(p, acc, sc, row0, col0, lane);
     else
-      epilogue_gated<TO, false, NI, NJ>(p, acc, sc, row0, col0, lane);
+      epilogue_gated<TO, false>(p, acc, sc, row0, col0, lane);
   } else {
     if (EPI != EPI_INT32 && p.bias)
-      epilogue_body<EPI, TO, VEC_OUT, true, NI, NJ>(p, acc, sc, row0, col0, lane);
+      epilogue_body<EPI, TO, VEC_OUT, true>(p, acc, sc, row0, col0, lane);
     else
-      epilogue_body<EPI, TO, VEC_OUT, false, NI, NJ>(p, acc, sc, row0, col0, lane);
+      epilogue_body<EPI, TO, VEC_OUT, false>(p, acc, sc, row0, col0, lane);
   }
 }
 
@@ -641,32 +677,26 @@ __device__ __forceinline__ void s_barrier() { asm volatile("s_barrier" ::: "memo
 // bias in TO, one rounding to TO). Host contract: N % 8 == 0, ldo % 8 == 0,
 // out 16-byte aligned.
 template <typename TO, bool BIAS>
-__device__ __forceinline__ void epilogue_rows_lds(const GemmArgs& p, v4i (&acc)[8][4], const EpiScalesT<8, 4>& sc,
+__device__ __forceinline__ void epilogue_rows_lds(const GemmArgs& p, v4i (&acc)[8][4], const LdsScales& sc,
                                                   int row0, int col0, int lane, int8_t* slice) {
   using S = typename TO::storage;
   const int q = lane >> 4, m16 = lane & 15;
-  float bv[4][4];
-  if constexpr (BIAS) {
-    const S* brow = static_cast<const S*>(p.bias);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) bv[j][r] = TO::load(brow[min(col0 + 4 * q + j * 16 + r, p.N - 1)]);
-  }
   const int rr = lane >> 3, ch = lane & 7;
   const int col = col0 + ch * 8;
   int8_t* wr = slice + m16 * 144 + 8 * q;
   const int8_t* rd = slice + rr * 144 + ch * 16;
   static_for<8>([&](auto I) {
     constexpr int i = I;
-    const float sxm = sc.sx[i];
+    const float sxm = sc.row(i);
     static_for<4>([&](auto J) {
       constexpr int j = J;
-      float v[4];
+      float v[4], sw[4], bv[4];
+      sc.col4(j, sw);
+      if constexpr (BIAS) sc.template bias4<TO>(p, 0, j, bv);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        float y = (float)acc[i][j][r] * (sxm * sc.sw[j][r]);
-        if constexpr (BIAS) y = TO::round(TO::round(y) + bv[j][r]);
+        float y = (float)acc[i][j][r] * (sxm * sw[r]);
+        if constexpr (BIAS) y = TO::round(TO::round(y) + bv[r]);
         v[r] = y;
       }
       uint2 w;
@@ -938,12 +968,14 @@ __global__ __launch_bounds__(PP_THREADS, 1) void gemm_i8_pp_kernel(GemmArgs p) {
     }
   }
   wait_vmcnt<0>();  // no DMA may land after the workgroup's LDS is released
-  EpiScalesT<8, 4> sc;
   const int row0 = m0 + wm * 128, col0 = n0 + wn * 64;
-  load_scales_t<EPI, 8, 4>(p, row0, col0, lane, sc);
   // The A ring is idle once P has passed its last barrier (every A DMA has
-  // landed and Q's last reads of it are done), so each wave's transpose slice
-  // lives there; the last refills of the other rings may still be landing.
+  // landed and Q's last reads of it are done), so each wave's scale region
+  // and transpose slice live there; the last refills of the other rings may
+  // still be landing.
+  static_assert(8 * PP_SLICE + 8 * LDS_SCALES_BYTES <= 2 * PP_TILE, "epilogue LDS exceeds the A ring");
+  const LdsScales sc = stage_scales<EPI, TO>(
+      p, row0, col0, lane, reinterpret_cast<float*>(lds + A0 + 8 * PP_SLICE + wave * LDS_SCALES_BYTES));
   if constexpr (EPI == EPI_DEQUANT && !std::is_same<TO, F32T>::value) {
     if (p.row_stores) {
       int8_t* slice = lds + A0 + wave * PP_SLICE;
