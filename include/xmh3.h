@@ -205,10 +205,12 @@ int xmh3_w4a8_gemm(const int8_t* A, int64_t lda, const uint8_t* packed, int64_t 
 
 /*
  * The W4A8 MLP block: grouped int4 weights (uniform levels, no rotation),
- * s_rel fp32 or bf16 [N, K/G], per-channel fp32 s_channel. Both weights are
- * decoded once per call to the int8 grid in the workspace (HBM-bound), then
- * the W8A8 chain runs; group_size is the weights' group (the workspace does
- * not depend on it).
+ * s_rel fp32 or bf16 [N, K/G], per-channel fp32 s_channel. Each weight is
+ * decoded once per call to the int8 grid (HBM-bound) into a workspace region
+ * that is idle while it is live, then the W8A8 chain runs: the workspace is
+ * the W8A8 one when M >= D (plus F*D bytes when M < D, plus another F*D when
+ * 2M < D). group_size is the weights' group (the workspace does not depend
+ * on it).
  * Replaces: the chunked W4A8 MLP (h3serve/native_engine/model/fused_mlp.py:222-266)
  * over w4a8_int8_linear (CK/tensor/w4a8_int8.py:89-115, eager
  * CK/backends/eager/w4a8_int8.py:457-508 decomposed as decode + int8_linear).

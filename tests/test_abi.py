@@ -52,9 +52,12 @@ def test_workspace_queries_without_gpu(pkg):
     for b in (25200 * 5120, 25200 * 4, 25200 * 13824 * 2, 25200 * 4, 25200 * 13824, 25200 * 4):
         expect += (b + 255) // 256 * 256
     assert n == expect
-    # the W8A8 regions plus both weights decoded to the int8 grid
-    w4 = lib.xmh3_w4a8_mlp_workspace_bytes(25200, 5120, 13824, 128)
-    assert w4 == n + (13824 * 5120 + 255) // 256 * 256 * 2
+    # W4A8 decodes W1 into q2's region (needs M >= d) and W2 into h's (2M >= d)
+    assert lib.xmh3_w4a8_mlp_workspace_bytes(25200, 5120, 13824, 128) == n
+    w8 = lib.xmh3_w8a8_mlp_workspace_bytes
+    assert lib.xmh3_w4a8_mlp_workspace_bytes(64, 256, 512, 128) == w8(64, 256, 512) + 2 * 512 * 256
+    assert lib.xmh3_w4a8_mlp_workspace_bytes(200, 256, 512, 64) == w8(200, 256, 512) + 512 * 256
+    assert lib.xmh3_w4a8_mlp_workspace_bytes(256, 256, 512, 16) == w8(256, 256, 512)
 
 
 def test_argument_errors_need_no_gpu(pkg):

@@ -355,6 +355,30 @@ def test_w4a8_linear_and_mlp(pkg, dev):
     close(ym, ymr, "w4a8 mlp")
 
 
+@pytest.mark.parametrize("m", [500, 1000, 2000])
+def test_w4a8_mlp_decoded_weights_share_the_workspace(pkg, dev, m):
+    """The W4A8 MLP decodes W1 into q2's workspace region and W2 into h's when
+    they fit (d=1536: W1 needs m >= 1536, W2 m >= 768), else into segments of
+    their own: at all three token counts it equals the W8A8 MLP on the decoded
+    weights bit for bit, from a workspace filled with garbage."""
+    say(f"w4a8 mlp workspace sharing m={m}")
+    from x_minimaxh3_amd import _lib, backend, workloads
+
+    inp = workloads.mlp_inputs(**workloads.CONFIGS["mlp_small"], seed=1, weights="w4a8")
+    x = inp["x"][:m].to(dev)
+    w = {k: inp[k].to(dev) for k in ("w1_packed", "w1_srel", "w1_schannel", "w2_packed", "w2_srel", "w2_schannel")}
+    d, f = x.shape[1], w["w1_packed"].shape[0]
+    nbytes = _lib.load().xmh3_w4a8_mlp_workspace_bytes(m, d, f, 128)
+    assert (nbytes == _lib.load().xmh3_w8a8_mlp_workspace_bytes(m, d, f)) == (m >= d)
+    ws = torch.full((nbytes,), 0x5A, dtype=torch.uint8, device=dev)
+    y = backend.w4a8_mlp(x, *w.values(), 128, workspace=ws)
+    w1 = backend.dequant_int4_grouped_to_int8(w["w1_packed"], w["w1_srel"], None, 128)
+    w2 = backend.dequant_int4_grouped_to_int8(w["w2_packed"], w["w2_srel"], None, 128)
+    want = backend.w8a8_mlp(x, w1, w["w1_schannel"], w2, w["w2_schannel"])
+    torch.cuda.synchronize()
+    assert same(y, want.cpu(), "w4a8 mlp vs w8a8 mlp on the decoded weights")
+
+
 @pytest.mark.parametrize("m,n,k,srel_dtype,srel_pad,bias", [
     (777, 1000, 768, torch.bfloat16, 1, False),
     (300, 512, 1024, torch.float32, 0, True),

@@ -12,11 +12,15 @@
 // GELU sits in step 3 rather than in the fc1 epilogue (the GEMM's epilogue
 // cannot overlap its MFMAs, while the row quantizer has VALU time to spare
 // under its memory traffic; measured 1.81 ms against 1.88 ms for steps 2-3 at
-// the 720p shape, identical codes). The W4A8 variant first turns both packed
-// int4 weights into the int8 grid.
+// the 720p shape, identical codes). The W4A8 variant first turns each packed
+// int4 weight into the int8 grid, in a workspace region that is idle while
+// that weight is live: W1 (before step 2) into q2's region, which step 3
+// overwrites only after fc1 has read W1; W2 (after step 3) into h's region,
+// which fc2 does not touch. A region too small for its weight (M < D for W1,
+// 2M < D for W2) gets a segment of its own at the end.
 // Workspace (caller-owned, 256-byte aligned segments):
 //   q1 [M,D] i8 | sx [M] f32 | h [M,F] bf16 | (unused) [M] u32 | q2 [M,F] i8 | sg [M] f32
-//   (+ W1 [F,D] i8 | W2 [D,F] i8 for W4A8)
+//   (+ W1 [F,D] i8 if M < D, + W2 [D,F] i8 if 2M < D, W4A8 only)
 #include "common.hpp"
 
 #include <mutex>
@@ -54,8 +58,9 @@ static MlpWs carve(void* base, int64_t M, int64_t D, int64_t F, bool w4) {
   auto take = [&](size_t n) { size_t o = off; off = align256(off + n); return o; };
   const size_t o_q1 = take((size_t)M * D), o_sx = take((size_t)M * 4), o_g = take((size_t)M * F * 2),
                o_am = take((size_t)M * 4), o_q2 = take((size_t)M * F), o_sg = take((size_t)M * 4);
-  size_t o_w1 = 0, o_w2 = 0;
-  if (w4) { o_w1 = take((size_t)F * D); o_w2 = take((size_t)D * F); }
+  size_t o_w1 = o_q2, o_w2 = o_g;
+  if (w4 && M < D) o_w1 = take((size_t)F * D);
+  if (w4 && 2 * M < D) o_w2 = take((size_t)D * F);
   w.bytes = off;
   char* b = static_cast<char*>(base);
   if (b) {
@@ -65,23 +70,36 @@ static MlpWs carve(void* base, int64_t M, int64_t D, int64_t F, bool w4) {
     w.amax = reinterpret_cast<uint32_t*>(b + o_am);
     w.q2 = reinterpret_cast<int8_t*>(b + o_q2);
     w.sg = reinterpret_cast<float*>(b + o_sg);
-    if (w4) { w.w1 = reinterpret_cast<int8_t*>(b + o_w1); w.w2 = reinterpret_cast<int8_t*>(b + o_w2); }
+    w.w1 = reinterpret_cast<int8_t*>(b + o_w1);
+    w.w2 = reinterpret_cast<int8_t*>(b + o_w2);
   }
   return w;
 }
 
-static int mlp_core(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
-                    const int8_t* w1, const float* s1, int s1_pc, const int8_t* w2, const float* s2,
-                    int s2_pc, void* y, int64_t ldy, const MlpWs& ws, hipStream_t st) {
+// Steps 1-3: q1, sx <- x; h <- fc1; q2, sg <- gelu(h).
+static int mlp_to_q2(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                     const int8_t* w1, const float* s1, int s1_pc, const MlpWs& ws, hipStream_t st) {
   int rc = quantize_rows(x, x_dtype, ACT_NONE, M, D, ldx, ws.q1, D, ws.sx, nullptr, st);
   if (rc) return rc;
   rc = int8_gemm(ws.q1, D, w1, D, M, F, D, ws.sx, s1, s1_pc, nullptr, ws.g, DT_BF16, F, 0 /*dequant*/,
                  nullptr, st);
   if (rc) return rc;
-  rc = quantize_rows(ws.g, DT_BF16, ACT_GELU_TANH, M, F, F, ws.q2, F, ws.sg, nullptr, st);
+  return quantize_rows(ws.g, DT_BF16, ACT_GELU_TANH, M, F, F, ws.q2, F, ws.sg, nullptr, st);
+}
+
+// Step 4: y <- fc2(q2).
+static int mlp_fc2(int64_t M, int64_t D, int64_t F, const int8_t* w2, const float* s2, int s2_pc, void* y,
+                   int64_t ldy, const MlpWs& ws, hipStream_t st) {
+  return int8_gemm(ws.q2, F, w2, F, M, D, F, ws.sg, s2, s2_pc, nullptr, y, DT_BF16, ldy, 0 /*dequant*/, nullptr,
+                   st);
+}
+
+static int mlp_core(const void* x, int x_dtype, int64_t M, int64_t D, int64_t F, int64_t ldx,
+                    const int8_t* w1, const float* s1, int s1_pc, const int8_t* w2, const float* s2,
+                    int s2_pc, void* y, int64_t ldy, const MlpWs& ws, hipStream_t st) {
+  int rc = mlp_to_q2(x, x_dtype, M, D, F, ldx, w1, s1, s1_pc, ws, st);
   if (rc) return rc;
-  return int8_gemm(ws.q2, F, w2, F, M, D, F, ws.sg, s2, s2_pc, nullptr, y, DT_BF16, ldy,
-                   0 /*dequant*/, nullptr, st);
+  return mlp_fc2(M, D, F, w2, s2, s2_pc, y, ldy, ws, st);
 }
 
 static int check_mlp_shapes(int64_t M, int64_t D, int64_t F, int64_t ldx, int64_t ldy) {
@@ -130,12 +148,15 @@ extern "C" int xmh3_w4a8_mlp(const void* x, int x_dtype, int64_t M, int64_t D, i
   XMH3_REQUIRE(workspace && workspace_bytes >= ws.bytes, "w4a8_mlp: workspace too small");
   XMH3_REQUIRE(x && w1_packed && w1_srel && w1_schannel && w2_packed && w2_srel && w2_schannel && y,
                "w4a8_mlp: null pointer");
+  // W1 may share q2's region and W2 h's region: the order below keeps each
+  // decoded weight intact until its GEMM has run (one stream)
   rc = w4_decode(w1_packed, w1_srel, srel_dtype, nullptr, F, D, group_size, ws.w1, stream);
+  if (rc) return rc;
+  rc = mlp_to_q2(x, x_dtype, M, D, F, ldx, ws.w1, w1_schannel, 1, ws, stream);
   if (rc) return rc;
   rc = w4_decode(w2_packed, w2_srel, srel_dtype, nullptr, D, F, group_size, ws.w2, stream);
   if (rc) return rc;
-  return mlp_core(x, x_dtype, M, D, F, ldx, ws.w1, w1_schannel, 1, ws.w2, w2_schannel, 1, y, ldy, ws,
-                  stream);
+  return mlp_fc2(M, D, F, ws.w2, w2_schannel, 1, y, ldy, ws, stream);
 }
 
 // ---------------------------------------------------------------------------
