@@ -18,6 +18,10 @@ starts):
     and H3's fc2 with the gated residual update in the GEMM epilogue (d=5376),
     against the same kernels with a separate addcmul_.
 
+Each measured section first runs its step untimed for at least 0.3 s (an
+idle GPU's clocks take tens of milliseconds of load to ramp back up), then
+the W warm-up steps, then the K timed steps.
+
 A step is one pass of the MLP block over the batch. The timed region runs the
 four MLP kernels (per-token quant, fc1 GEMM + dequant epilogue, GELU + per-token
 quant, fc2 GEMM + dequant) through the C ABI on torch's current stream, with
@@ -50,14 +54,27 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 # 0.5 GiB by FETCH_SIZE and 1 GiB by WRITE_SIZE, so FETCH_SIZE is scaled x2 and
 # WRITE_SIZE x1 (see profiles/).
 TRAFFIC_BYTES = {
-    "fc1_gemm": (1460067.6 * 2 + 691096.8) * 1024,
-    "fc2_gemm": (1475146.7 * 2 + 255960.1) * 1024,
-    "norm_rope": (265152.6 * 2 + 504021.2) * 1024,
+    "fc1_gemm": (1619000.0 * 2 + 680400.0) * 1024,
+    "fc2_gemm": (1473000.0 * 2 + 252000.0) * 1024,
+    "norm_rope": (265100.0 * 2 + 504000.0) * 1024,
 }
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def host_cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline_mlp(inp: dict, sample_rows: int, repeats: int = 3) -> dict:
@@ -78,7 +95,7 @@ def cpu_baseline_mlp(inp: dict, sample_rows: int, repeats: int = 3) -> dict:
     t = statistics.median(times)
     d, f = inp["x"].shape[1], inp["w1"].shape[0]
     return {"value": round(4.0 * sample_rows * d * f / t / 1e12, 4), "unit": "TOPS",
-            "cores": torch.get_num_threads(), "kind": "port",
+            "cores": torch.get_num_threads(), "kind": "port", "cpu_model": host_cpu_model(),
             "sample": f"oracle w8a8_mlp on {sample_rows} of {inp['x'].shape[0]} tokens, full {d}->{f}->{d} "
                       f"weights, median of {repeats} runs ({t:.2f} s each), torch {torch.__version__}"}
 
@@ -97,13 +114,30 @@ def cpu_baseline_norm_rope(nr: dict, repeats: int = 3) -> dict:
     t = statistics.median(times)
     m, d = nr["q"].shape
     return {"value": round(8.0 * m * d / t / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port", "sample": f"oracle norm_rope on Q and K, full {m}x{d}, median of {repeats}"}
+            "kind": "port", "cpu_model": host_cpu_model(), "sample": f"oracle norm_rope on Q and K, full {m}x{d}, median of {repeats}"}
+
+
+def settle(fn, min_s: float = 0.3) -> None:
+    """Run `fn` untimed for at least `min_s` seconds before its warm-up steps.
+    An MI355X that has been idle (input generation, a host-side phase) takes
+    tens of milliseconds of sustained load to bring its clocks back up: in a
+    kernel trace of this bench the 720p fc1 GEMM ran 1.86, 1.63, 1.52 ... ms
+    over its first launches and settled at 1.37 ms after about twelve."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min_s:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
 
 
 def timed(fn, steps: int, warmup: int) -> float:
     """Median ms of `fn` over `steps` launches, HIP events on the current stream."""
     import torch
 
+    settle(fn)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -259,7 +293,7 @@ def bench_long(pkg, dev, inp: dict, warmup: int) -> dict:
     w1, s1, w2, s2 = (inp[k_].to(dev) for k_ in ("w1", "s1", "w2", "s2"))
     drv = driver.LongBlockDriver(w1, s1, w2, s2, scale, shift, chunk=chunk)
     qo, ko, y = torch.empty_like(q), torch.empty_like(k), torch.empty(m, d, dtype=torch.bfloat16, device=dev)
-    ms_res = timed(lambda: drv.run_resident(q, k, x, freqs, qo, ko, y), 3, max(1, warmup // 2))
+    ms_res = timed(lambda: drv.run_resident(q, k, x, freqs, qo, ko, y), 5, max(1, warmup // 2))
     # streamed: the same tensors in pinned host memory
     host = {n: torch.empty(m, d, dtype=torch.bfloat16, pin_memory=True) for n in ("q", "k", "x", "qo", "ko", "y")}
     host["q"].copy_(q)
@@ -355,6 +389,7 @@ def main() -> int:
         if ev:
             ev[4].record()
 
+    settle(lambda: step(None))
     for _ in range(args.warmup):
         step(None)
     torch.cuda.synchronize()
@@ -386,6 +421,7 @@ def main() -> int:
         _lib.call("xmh3_norm_rope", qd.data_ptr(), qo.data_ptr(), kd.data_ptr(), ko.data_ptr(), 2, Mn, Dn, Dn, Dn,
                   scd.data_ptr(), shd.data_ptr(), 2, Dn, Mn, ft.data_ptr(), 0, ft.stride(0), 128, 1e-6, st)
 
+    settle(nr_step)
     for _ in range(args.warmup):
         nr_step()
     torch.cuda.synchronize()
@@ -403,7 +439,7 @@ def main() -> int:
     # ------------------------------------------------------------------ W4A8 and long sequence
     w4 = long = cr = h3fc2 = h3norm = None
     if not args.no_extra:
-        w4 = bench_w4a8(pkg, dev, max(3, args.steps // 4), 2)
+        w4 = bench_w4a8(pkg, dev, args.steps, args.warmup)
         log(f"w4a8 mlp: {w4['ms_per_step']:.3f} ms/step ({w4['value']} TOPS)")
         cr = bench_convrot(pkg, dev, args.steps, args.warmup)
         log(f"convrot swiglu quant: {cr['us_per_launch']:.1f} us/launch, {cr['achieved']:.0f} GB/s")
@@ -446,12 +482,12 @@ def main() -> int:
                    "norm_rope_workload": "norm_rope_720p", "grid": [7, 45, 80], "heads": 40, "head_dim": 128},
         "frac_of_peak": round(tops / PEAK_INT8_TOPS, 4),
         "kernels_ms": {k: round(v, 4) for k, v in kavg.items()},
-        "roofline": {"kernel": "gemm_i8_v5_kernel (fc1, dequant epilogue)", "bound": "mfma",
+        "roofline": {"kernel": "gemm_i8_pp_kernel (fc1, dequant epilogue)", "bound": "mfma",
                      "achieved": round(fc1_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                      "frac": round(fc1_tops / PEAK_INT8_TOPS, 4),
                      "traffic": round(TRAFFIC_BYTES["fc1_gemm"]),
                      "algorithmic": "2*M*d*ffn int8 ops per launch (unit: 1e12 int8 ops/s)"},
-        "roofline_fc2": {"kernel": "gemm_i8_v5_kernel (fc2, dequant epilogue)", "bound": "mfma",
+        "roofline_fc2": {"kernel": "gemm_i8_pp_kernel (fc2, dequant epilogue)", "bound": "mfma",
                          "achieved": round(fc2_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                          "frac": round(fc2_tops / PEAK_INT8_TOPS, 4),
                          "traffic": round(TRAFFIC_BYTES["fc2_gemm"])},
