@@ -51,6 +51,19 @@ int xmh3_quantize_int8_rowwise(const void* x, int x_dtype, int input_act, int64_
                                int64_t ldx, int8_t* q, float* scale, xmh3_stream_t stream);
 
 /*
+ * quantize_int8_rowwise with the stochastic_rounding seed: stochastic == 0 is
+ * xmh3_quantize_int8_rowwise (no input act); otherwise each code is
+ * floor(T(v + T(u))) with v = T(x / T(s)) as in the nearest path and
+ * u = (pcg(lo32(k) ^ hi32(k)) >> 8) * 2^-24, k = row * K + col + seed
+ * (uint64), pcg the 32-bit PCG-RXS-M-XS output hash: the reference CUDA
+ * quantizer's deterministic noise. Scales as xmh3_quantize_int8_rowwise.
+ * Replaces: the rowwise quantizer launcher with stochastic = true, seed
+ * (CK/backends/cuda/ops/int8_linear.cu:1035-1075, kernel :158-197).
+ */
+int xmh3_quantize_int8_rowwise_sr(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q,
+                                  float* scale, int stochastic, uint64_t seed, xmh3_stream_t stream);
+
+/*
  * As xmh3_quantize_int8_rowwise, and also writes 0 to clear_rows[0..M) (the
  * row-|max| slots the fused MLP's fc1 epilogue accumulates into; NULL = none):
  * the first kernel of the MLP chain. Same reference interface as above.

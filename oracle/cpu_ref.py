@@ -17,7 +17,13 @@ live in ``tests/test_oracle.py``):
 
 * ``quantize_int8_rowwise``  -- numpy restatement (``npref``), the C
   restatement (``c/oracle.c``) and hand-built special cases (zero row,
-  -127.5 -> -128, +127.5 -> 127, half-to-even ties).
+  -127.5 -> -128, +127.5 -> 127, half-to-even ties). Its stochastic form:
+  the C restatement of the bf16 case (fp32 add then one bf16 rounding, a
+  different route to the same single rounding), ``round_to_dtype`` against
+  torch's own fp32 -> bf16 / fp16 conversions, the keying identities of the
+  noise (seed + 1 at idx == seed at idx + 1; the 64-bit fold), the range
+  and uniformity of the hash output, codes in {floor(v), floor(v) + 1} and
+  their mean over seeds against v (unbiasedness).
 * ``int8_mm``                -- int64 brute force (numpy and C).
 * ``dequant``/``int8_linear``-- float64 closed form + the C restatement of
   the fp32 epilogue; composite order vs a step-by-step numpy restatement.
@@ -51,6 +57,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -69,20 +76,67 @@ def _int8_scale_for_math(scale: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     return torch.where(scale == 0, torch.full_like(scale, tiny), scale)
 
 
-def quantize_int8_rowwise(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """CK/backends/eager/quantization.py:857-875 (with _round_int8 :821-826,
-    stochastic_rounding=0).
+def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """CK/backends/eager/quantization.py:857-875 (with _round_int8 :821-826).
 
     amax in x's dtype; scale = max(amax.float()/127, 1e-30) (fp32, true
     division); v = x / scale.to(x.dtype) in x's dtype; round half to even;
     clamp [-128, 127]. Returns (int8 [...,K], fp32 [...,1]) with the
     unrounded fp32 scale.
+
+    stochastic_rounding = seed > 0: v as above, then floor(T(v + noise)) with
+    the reference CUDA quantizer's deterministic noise of each element
+    (``stochastic_noise``; CK/backends/cuda/ops/int8_linear.cu:186-195), the
+    sum rounded once to x's dtype. The eager backend draws its noise from a
+    seeded torch generator (:803-812), whose stream depends on the device and
+    the torch build, so its stochastic codes cannot be reproduced elsewhere;
+    the CUDA backend's hash is the reproducible definition.
     """
     abs_max = x.abs().amax(dim=-1, keepdim=True)
     scale = (abs_max.float() / 127.0).clamp(min=1e-30)
     scaled = x / _int8_scale_for_math(scale, x)
+    if stochastic_rounding is not None and stochastic_rounding > 0:
+        idx = np.arange(x.numel(), dtype=np.uint64)          # row * K + col of the [..., K] matrix
+        noise = stochastic_noise(idx, int(stochastic_rounding), x.dtype).reshape(tuple(x.shape))
+        summed = round_to_dtype(scaled.double().numpy() + noise, x.dtype)   # exact sum, one rounding
+        q = torch.from_numpy(np.floor(summed)).clamp_(-128.0, 127.0).to(torch.int8)
+        return q, scale
     q = scaled.round_().clamp_(-128.0, 127.0).to(torch.int8)
     return q, scale
+
+
+def pcg_hash(x: np.ndarray) -> np.ndarray:
+    """The 32-bit PCG-RXS-M-XS output hash (O'Neill's PCG family, as the GPU
+    hash of Jarzynski and Olano, "Hash Functions for GPU Rendering", JCGT 9(3)
+    2020) that keys the reference's stochastic rounding noise
+    (CK/backends/cuda/ops/int8_linear.cu:79-83). uint32 in, uint32 out."""
+    x = np.asarray(x, dtype=np.uint32)
+    with np.errstate(over="ignore"):
+        state = x * np.uint32(747796405) + np.uint32(2891336453)
+        word = ((state >> ((state >> np.uint32(28)) + np.uint32(4))) ^ state) * np.uint32(277803737)
+    return (word >> np.uint32(22)) ^ word
+
+
+def round_to_dtype(x64: np.ndarray, dtype: torch.dtype) -> np.ndarray:
+    """float64 values -> the nearest value of ``dtype`` (bf16, fp16 or fp32),
+    ties to even, in one rounding, subnormals included; returned as float64."""
+    p, emin = {torch.bfloat16: (8, -126), torch.float16: (11, -14), torch.float32: (24, -126)}[dtype]
+    x64 = np.asarray(x64, dtype=np.float64)
+    _, e = np.frexp(x64)                                   # x = m * 2^e, 0.5 <= |m| < 1
+    quantum = np.maximum(e - 1, emin) - (p - 1)            # exponent of the last significand bit
+    return np.ldexp(np.rint(np.ldexp(x64, -quantum)), quantum)
+
+
+def stochastic_noise(idx: np.ndarray, seed: int, dtype: torch.dtype) -> np.ndarray:
+    """CK/backends/cuda/ops/int8_linear.cu:85-91: key = idx + seed (uint64,
+    wrapping), folded = lo32(key) ^ hi32(key), u = (pcg_hash(folded) >> 8) *
+    2^-24 in [0, 1), rounded to ``dtype`` (bf16 can round it up to 1.0).
+    float64 out."""
+    with np.errstate(over="ignore"):
+        key = np.asarray(idx, dtype=np.uint64) + np.uint64(seed)
+    folded = ((key & np.uint64(0xFFFFFFFF)) ^ (key >> np.uint64(32))).astype(np.uint32)
+    u = (pcg_hash(folded) >> np.uint32(8)).astype(np.float64) * 2.0 ** -24
+    return round_to_dtype(u, dtype)
 
 
 # ---------------------------------------------------------------------------

@@ -46,14 +46,16 @@ def corc():
     import subprocess
 
     so = ROOT / "oracle" / "_build" / "liboracle.so"
-    if not so.exists():
-        subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)   # rebuilds if oracle.c changed
     lib = ctypes.CDLL(str(so))
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     lib.orc_quant_rows_bf16.argtypes = [vp, i64, i64, vp, vp]
     lib.orc_int_mm.argtypes = [vp, vp, i64, i64, i64, vp]
     lib.orc_dequant_bf16.argtypes = [vp, vp, vp, ctypes.c_int, i64, i64, vp]
     lib.orc_w4_decode.argtypes = [vp, vp, i64, i64, i64, vp]
-    for f in (lib.orc_quant_rows_bf16, lib.orc_int_mm, lib.orc_dequant_bf16, lib.orc_w4_decode):
+    lib.orc_pcg_hash.argtypes = [vp, i64, vp]
+    lib.orc_quant_rows_sr_bf16.argtypes = [vp, i64, i64, ctypes.c_uint64, vp, vp]
+    for f in (lib.orc_quant_rows_bf16, lib.orc_int_mm, lib.orc_dequant_bf16, lib.orc_w4_decode, lib.orc_pcg_hash,
+              lib.orc_quant_rows_sr_bf16):
         f.restype = None
     return lib

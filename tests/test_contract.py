@@ -57,7 +57,9 @@ def test_unimplemented_reference_features_raise(pkg):
     with pytest.raises(ValueError, match="per-output-channel"):
         backend.int8_linear(x, w, torch.ones(3))
     with pytest.raises(NotImplementedError, match="stochastic"):
-        backend.quantize_int8_rowwise(x, stochastic_rounding=5)
+        backend.quantize_int8_rowwise_convrot64(x, 256, stochastic_rounding=5)
+    with pytest.raises(ValueError, match="64 bits"):
+        backend.quantize_int8_rowwise(x, stochastic_rounding=1 << 64)
 
 
 def test_w4a8_operand_validation(pkg):

@@ -80,6 +80,38 @@ def test_quantize_bit_exact(pkg, dev, m, k, dtype):
     assert torch.equal(q.cpu(), qr), (q.cpu() != qr).sum().item()
 
 
+@pytest.mark.parametrize("shape,dtype,seed,strided", [
+    ((300, 1536), torch.bfloat16, 1, False),
+    ((2, 150, 777), torch.bfloat16, (9 << 32) + 12345, False),   # 3-D, ragged K, seed past 2^32
+    ((64, 5120), torch.float16, 42, False),
+    ((33, 520), torch.float32, 7, False),
+    ((40, 1000), torch.bfloat16, 3, True),                       # row stride 1024
+    ((1, 13824), torch.bfloat16, 2 ** 64 - 5, False),           # the index + seed wraps
+])
+def test_quantize_stochastic_bit_exact(pkg, dev, shape, dtype, seed, strided):
+    """stochastic_rounding=seed: codes and scales equal the oracle's (the
+    reference CUDA quantizer's hash noise, one rounding of the sum to the row
+    dtype, floor), including 3-D inputs, a strided view and seeds whose
+    64-bit key wraps or folds its high word."""
+    say(f"quantize stochastic {shape} {dtype} seed={seed} strided={strided}")
+    g = torch.Generator().manual_seed(len(shape) * 1000 + shape[-1])
+    x = torch.randn(*shape, generator=g)
+    x[..., : max(1, shape[-1] // 100)] *= 20
+    x = x.to(dtype)
+    xd = x.to(dev)
+    if strided:
+        wide = torch.zeros(shape[0], 1024, dtype=dtype, device=dev)
+        wide[:, : shape[-1]] = xd
+        xd = wide[:, : shape[-1]]
+    q, s = pkg.quantize_int8_rowwise(xd, stochastic_rounding=seed)
+    torch.cuda.synchronize()
+    qr, sr = cpu_ref.quantize_int8_rowwise(x, seed)
+    assert torch.equal(s.cpu(), sr)
+    assert same(q, qr, "stochastic codes")
+    q0, _ = pkg.quantize_int8_rowwise(xd)
+    assert not torch.equal(q.cpu(), q0.cpu())
+
+
 def test_quantize_minus_128_cases(pkg, dev):
     say("quantize -128 cases")
     vals = torch.arange(0x3f80, 0x4000, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)

@@ -89,6 +89,100 @@ def test_quant_reaches_minus_128_and_clamps_plus_127():
     assert hits, "the [-128, 127] clamp range is never exercised"
 
 
+def test_stochastic_hash_matches_c_and_fills_24_bits(corc):
+    """The noise hash: the numpy and C restatements agree on 2^20 inputs; its
+    top 24 bits (the noise) span [0, 2^24) and are uniform over 256 buckets
+    (chi-square, 255 degrees of freedom, far below the 0.1 % tail)."""
+    import ctypes
+
+    x = np.random.default_rng(1).integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)
+    x[:4] = (0, 1, 0xFFFFFFFF, 0x80000000)
+    h = cpu_ref.pcg_hash(x)
+    hc = np.empty_like(x)
+    corc.orc_pcg_hash(x.ctypes.data_as(ctypes.c_void_p), x.size, hc.ctypes.data_as(ctypes.c_void_p))
+    assert np.array_equal(h, hc)
+    u = h >> np.uint32(8)
+    assert u.max() > (1 << 24) - 64 and u.min() < 64
+    counts = np.bincount((u >> np.uint32(16)).astype(np.int64), minlength=256)
+    e = x.size / 256
+    assert ((counts - e) ** 2 / e).sum() < 330.0
+
+
+def test_round_to_dtype_matches_torch_conversions():
+    """round_to_dtype (one rounding from float64) equals torch's fp32 -> bf16 /
+    fp16 conversions on fp32 inputs, subnormals, ties and overflow-free
+    extremes included; fp32 values are fixed points."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.cat((torch.randn(20000, generator=g) * 100, torch.rand(20000, generator=g) * 2 ** -13,
+                   torch.tensor([0.0, -0.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 2 ** -24, 3 * 2 ** -25, 65504.0])))
+    x64 = x.double().numpy()
+    for dt in (torch.bfloat16, torch.float16):
+        assert np.array_equal(cpu_ref.round_to_dtype(x64, dt), x.to(dt).double().numpy()), dt
+    assert np.array_equal(cpu_ref.round_to_dtype(x64, torch.float32), x64)
+
+
+def test_stochastic_noise_keying():
+    """key = idx + seed: seed + 1 at idx equals seed at idx + 1; seeds past
+    2^32 fold their high word in by xor: (a << 32 | b) at idx equals seed
+    (b + idx) ^ a at index 0; the noise lies in [0, 1] and only bf16 can
+    round it up to 1."""
+    idx = np.arange(5000, dtype=np.uint64)
+    for dt in (torch.bfloat16, torch.float16, torch.float32):
+        n1 = cpu_ref.stochastic_noise(idx, 1234, dt)
+        assert np.array_equal(cpu_ref.stochastic_noise(idx, 1235, dt)[:-1], n1[1:])
+        assert n1.min() >= 0.0 and n1.max() <= 1.0
+        a, b = 7, 1000
+        folded = cpu_ref.stochastic_noise(idx[:100], (a << 32) | b, dt)
+        direct = np.array([cpu_ref.stochastic_noise(np.zeros(1, np.uint64), (b + i) ^ a, dt)[0] for i in range(100)])
+        assert np.array_equal(folded, direct)
+    assert cpu_ref.stochastic_noise(np.arange(1 << 16, dtype=np.uint64), 1, torch.float32).max() < 1.0
+
+
+def test_stochastic_quant_matches_c_and_is_unbiased(corc):
+    """bf16 rows: the oracle's stochastic codes equal the C restatement's for
+    several seeds (including one past 2^32); every code is floor(v) or
+    floor(v) + 1 of the nearest path's v = bf16(x / bf16(s)); the mean code
+    over 400 seeds is within 5 sigma of v where bf16 resolves the sum finely
+    (|v| < 2: the reference rounds v + noise to bf16, whose step is 2^-6 at
+    2 and 0.5 at 64, so larger codes are biased by design); seed 0 is the
+    nearest path. fp32 rows are unbiased at every magnitude."""
+    import ctypes
+
+    x = outlier_acts(6, 300, seed=9, n_out=3)
+    q0, s0 = cpu_ref.quantize_int8_rowwise(x)
+    assert torch.equal(cpu_ref.quantize_int8_rowwise(x, 0)[0], q0)
+    v = (x / cpu_ref._int8_scale_for_math(s0, x)).double()
+    xb = bits(x)
+    for seed in (1, 77, (5 << 32) + 3):
+        q, s = cpu_ref.quantize_int8_rowwise(x, seed)
+        qc = np.empty((6, 300), np.int8)
+        sc = np.empty(6, np.float32)
+        corc.orc_quant_rows_sr_bf16(xb.ctypes.data_as(ctypes.c_void_p), 6, 300, seed,
+                                    qc.ctypes.data_as(ctypes.c_void_p), sc.ctypes.data_as(ctypes.c_void_p))
+        assert np.array_equal(q.numpy(), qc) and np.array_equal(s.numpy()[:, 0], sc) and torch.equal(s, s0)
+        d = q.double() - v.floor().clamp(-128, 127)
+        assert ((d == 0) | (d == 1)).all()
+    acc = torch.zeros_like(v)
+    for seed in range(1, 401):
+        acc += cpu_ref.quantize_int8_rowwise(x, seed)[0].double()
+    mean = acc / 400
+    inner = v.abs() < 2
+    frac = v - v.floor()
+    sigma = (frac * (1 - frac) / 400).sqrt()
+    assert inner.float().mean() > 0.2
+    assert ((mean - v).abs()[inner] <= 5 * sigma[inner] + 2 ** -6).all()
+    xf = x.float()
+    q0f, s0f = cpu_ref.quantize_int8_rowwise(xf)
+    vf = (xf / s0f).double()
+    accf = torch.zeros_like(vf)
+    for seed in range(1, 401):
+        accf += cpu_ref.quantize_int8_rowwise(xf, seed)[0].double()
+    fracf = vf - vf.floor()
+    inner = (vf > -127) & (vf < 126)
+    sig = (fracf * (1 - fracf) / 400).sqrt()
+    assert ((accf / 400 - vf).abs()[inner] <= 5 * sig[inner] + 2 ** -20).all()
+
+
 def test_quant_half_to_even_ties():
     # row amax 127 -> scale exactly 1.0 in fp32 and bf16; values k + 0.5
     # (bf16-exact) divide exactly and must round to even

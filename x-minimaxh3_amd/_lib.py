@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple] = {
     "xmh3_last_error": (ctypes.c_char_p, []),
     "xmh3_abi_version": (c_int, []),
     "xmh3_quantize_int8_rowwise": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p]),
+    "xmh3_quantize_int8_rowwise_sr": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_int,
+                                              ctypes.c_uint64, c_void_p]),
     "xmh3_quantize_int8_rowwise_ex": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_void_p, c_void_p,
                                               c_void_p, c_void_p]),
     "xmh3_quantize_int8_rowwise_convrot": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_void_p,

@@ -338,6 +338,57 @@ __global__ __launch_bounds__(256) void requant_rows_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// stochastic rounding (the reference CUDA quantizer's rule,
+// CK/backends/cuda/ops/int8_linear.cu:79-91,186-195): element idx = row*K +
+// col of the logical [M, K] matrix draws u = (h >> 8) * 2^-24 in [0, 1) with
+// h = PCG-RXS-M-XS(lo32(idx + seed) ^ hi32(idx + seed)), rounded to T; its
+// code is floor(T(v + T(u))) with v = T(x / T(s)) as in the nearest path.
+// The sum is added in fp32 and rounded once to T, which equals T's single
+// rounding of the exact sum: when the exact sum of two T values does not fit
+// fp32's 24 bits, the smaller one lies below 2^-15 (bf16; 2^-12 for fp16) of
+// the larger and cannot reach T's half-step, while every T tie is an exact
+// fp32 sum. One block per row; the second pass re-reads the row (mostly
+// from L2).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pcg_output_hash(uint32_t x) {
+  const uint32_t state = x * 747796405u + 2891336453u;
+  const uint32_t word = ((state >> ((state >> 28u) + 4u)) ^ state) * 277803737u;
+  return (word >> 22u) ^ word;
+}
+
+template <typename T>
+__device__ __forceinline__ float sr_noise(uint64_t idx, uint64_t seed) {
+  const uint64_t key = idx + seed;
+  const uint32_t h = pcg_output_hash((uint32_t)key ^ (uint32_t)(key >> 32));
+  return T::round((float)(h >> 8) * 0x1.0p-24f);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rows_sr_kernel(
+    const typename T::storage* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
+    int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale, uint64_t seed) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const typename T::storage* xr = x + row * ldx;
+  float amax = 0.0f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) amax = fmaxf(amax, fabsf(T::load(xr[k])));
+  amax = wave_max(amax);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = row_scale(amax);
+  const float sT = scale_for_math<T>(s);
+  int8_t* qr = q + row * ldq;
+  const uint64_t base = (uint64_t)row * (uint64_t)K;
+  for (int64_t k = threadIdx.x; k < K; k += 256) {
+    const float v = T::round(T::load(xr[k]) / sT);
+    const float c = floorf(T::round(v + sr_noise<T>(base + (uint64_t)k, seed)));
+    qr[k] = (int8_t)fminf(fmaxf(c, -128.0f), 127.0f);
+  }
+  if (threadIdx.x == 0) scale[row] = s;
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 template <typename T, int ACT>
@@ -401,6 +452,33 @@ int quantize_rows(const void* x, int x_dtype, int input_act, int64_t M, int64_t 
   }
 }
 
+int quantize_rows_sr(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int8_t* q, int64_t ldq,
+                     float* scale, uint64_t seed, hipStream_t st) {
+  XMH3_REQUIRE(M >= 0 && K >= 0, "quantize_int8_rowwise: negative size");
+  XMH3_REQUIRE(M < (1LL << 31), "quantize_int8_rowwise: too many rows for stochastic rounding");
+  if (M == 0) return XMH3_OK;
+  XMH3_REQUIRE(x && q && scale, "quantize_int8_rowwise: null pointer");
+  XMH3_REQUIRE(ldx >= K && ldq >= K, "quantize_int8_rowwise: leading dimension < K");
+  const dim3 grid((unsigned)M), block(256);
+  switch (x_dtype) {
+    case DT_BF16:
+      hipLaunchKernelGGL((quant_rows_sr_kernel<BF16T>), grid, block, 0, st, static_cast<const uint16_t*>(x), ldx,
+                         M, K, q, ldq, scale, seed);
+      break;
+    case DT_F16:
+      hipLaunchKernelGGL((quant_rows_sr_kernel<F16T>), grid, block, 0, st, static_cast<const uint16_t*>(x), ldx,
+                         M, K, q, ldq, scale, seed);
+      break;
+    case DT_F32:
+      hipLaunchKernelGGL((quant_rows_sr_kernel<F32T>), grid, block, 0, st, static_cast<const float*>(x), ldx, M,
+                         K, q, ldq, scale, seed);
+      break;
+    default:
+      return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise: dtype must be fp32, fp16 or bf16");
+  }
+  return check_launch("quant_rows_sr_kernel");
+}
+
 int requant_rows(const void* g, int g_dtype, int64_t M, int64_t K, int64_t ldg,
                  const uint32_t* row_amax, int8_t* q, int64_t ldq, float* scale, hipStream_t st) {
   XMH3_REQUIRE(M >= 0 && K >= 0, "requant: negative size");
@@ -434,6 +512,13 @@ extern "C" int xmh3_quantize_int8_rowwise_ex(const void* x, int x_dtype, int inp
                                              int64_t K, int64_t ldx, int8_t* q, float* scale,
                                              uint32_t* clear_rows, hipStream_t stream) {
   return xmh3::quantize_rows(x, x_dtype, input_act, M, K, ldx, q, K, scale, clear_rows, stream);
+}
+
+extern "C" int xmh3_quantize_int8_rowwise_sr(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                                             int8_t* q, float* scale, int stochastic, uint64_t seed,
+                                             hipStream_t stream) {
+  if (!stochastic) return xmh3::quantize_rows(x, x_dtype, 0, M, K, ldx, q, K, scale, nullptr, stream);
+  return xmh3::quantize_rows_sr(x, x_dtype, M, K, ldx, q, K, scale, seed, stream);
 }
 
 extern "C" int xmh3_requant_int8_rows(const void* g, int g_dtype, int64_t M, int64_t K, int64_t ldg,

@@ -162,7 +162,7 @@ def quantize_int8_rowwise(x: torch.Tensor, stochastic_rounding: int | None = 0):
     """Quantize tensor to INT8 with per-row scales -> (int8 like x, fp32 [..., 1])."""
     if stochastic_rounding:
         kw = {"x": x, "stochastic_rounding": stochastic_rounding}
-        return _impl("quantize_int8_rowwise", kw)(**kw)  # raises NotImplementedError
+        return _impl("quantize_int8_rowwise", kw)(**kw)
     return torch.ops.x_minimaxh3_amd.quantize_int8_rowwise(x)
 
 
