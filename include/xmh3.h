@@ -285,16 +285,31 @@ int xmh3_rope_split_half(void* x, void* out, int dtype, int64_t B, int64_t S, in
                          int norm, xmh3_stream_t stream);
 
 /*
+ * xmh3_rope_split_half with the pair layout chosen: split_half = 1 pairs
+ * (i, i + rot_dim/2), split_half = 0 the interleaved pairs (2i, 2i + 1) of
+ * CK/backends/eager/rope.py:10-16 (rotation f[.,0]*x0 then addcmul_ of
+ * f[.,1]*x1, one fused multiply-add in the table dtype), rot_dim and
+ * head_dim multiples of 8. Same operands otherwise.
+ * Replaces: CK/backends/cuda/ops/rms_rope.cu:353-384 launch_rms_rope_kernel
+ *   (both modes), eager CK/backends/eager/rope.py:10-36 (apply_rope*) and
+ *   67-118,146-167 (rms_rope*).
+ */
+int xmh3_rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                    const int64_t* x_strides, const int64_t* out_strides, const void* norm_weight,
+                    int weight_dtype, const void* freqs, int freqs_dtype, const int64_t* freqs_strides,
+                    int rot_dim, float eps, int norm, int split_half, xmh3_stream_t stream);
+
+/*
  * The reference's per-head RMSNorm + RoPE launcher under its own name and
  * 46-argument list (7 pointers; batch, dim1, dim2, head_dim, rot_dim; the
  * table's three leading sizes; 4 strides each of q, k, q_out, k_out; 6 table
  * strides; the q / k weight strides; epsilon; input, table and weight dtype
  * codes; has_k; split_half; stream), so a ctypes caller with pinned argtypes
  * (h3serve/native_engine/model/single_qknorm_rope.py:36-66,158-187) binds
- * this library unchanged. Runs the head-span kernel of xmh3_rope_split_half.
- * Returns nothing, as the reference does: an argument outside this build's
- * support (interleaved pairs, a strided head dimension, weight or table pair
- * layout) launches nothing and sets xmh3_last_error().
+ * this library unchanged. Runs the head-span kernel of xmh3_rope_heads in
+ * either pair layout. Returns nothing, as the reference does: an argument
+ * outside this build's support (a strided head dimension, weight or table
+ * pair layout) launches nothing and sets xmh3_last_error().
  * Replaces: CK/backends/cuda/ops/rms_rope.cu:353-384 launch_rms_rope_kernel.
  */
 void launch_rms_rope_kernel(const void* q, const void* k, const void* freqs, const void* q_scale,

@@ -51,6 +51,11 @@ live in ``tests/test_oracle.py``):
   times theta^(-2i/dim)) and the unit-modulus invariant.
 * ``apply_rope_split_half1`` -- complex-multiplication form, identity table
   reduces to the input, norm-preservation invariant.
+* ``apply_rope1`` / ``rms_rope1`` (interleaved pairs) -- the split-half form
+  on the de-interleaved head (same rotation, pairs regrouped) within one
+  rounding of the table dtype, the addcmul_ step equal to a float64 fused
+  multiply-add rounded once, identity table reduces to the input (or to
+  ``F.rms_norm``).
 """
 
 from __future__ import annotations
@@ -514,6 +519,31 @@ def rms_rope_split_half1(x: torch.Tensor, freqs_cis: torch.Tensor, weight: torch
         rotated = apply_rope_split_half1(x_norm[..., :rot_dim], freqs_cis)
         return torch.cat((rotated, x_norm[..., rot_dim:]), dim=-1)
     return apply_rope_split_half1(x_norm, freqs_cis)
+
+
+def apply_rope1(x: torch.Tensor, freqs_cis: torch.Tensor) -> torch.Tensor:
+    """CK/backends/eager/rope.py:10-16: interleaved pairs (2i, 2i+1) in the
+    table's dtype: out_r = f[r, 0] * x0, then addcmul_(f[r, 1], x1) (torch's
+    CPU addcmul evaluates that as one fused multiply-add), cast back. The
+    table is trimmed to x's sequence dim as the reference does
+    (CK/_rope_utils.py:4-13)."""
+    x_ = x.to(dtype=freqs_cis.dtype).reshape(*x.shape[:-1], -1, 1, 2)
+    if x.ndim > 2 and freqs_cis.ndim > 2 and x.shape[2] != 1 and freqs_cis.shape[2] > x.shape[2]:
+        freqs_cis = freqs_cis[:, :, : x.shape[2]]
+    x_out = freqs_cis[..., 0] * x_[..., 0]
+    x_out.addcmul_(freqs_cis[..., 1], x_[..., 1])
+    return x_out.reshape(*x.shape).type_as(x)
+
+
+def rms_rope1(x: torch.Tensor, freqs_cis: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+              rot_dim: int = 0) -> torch.Tensor:
+    """CK/backends/eager/rope.py:67-101 (split_half=False): per-head
+    F.rms_norm with weight, then the interleaved rotation of the first
+    rot_dim dims (0 = all), the tail norm-only."""
+    x_norm = F.rms_norm(x, (x.shape[-1],), weight=weight, eps=eps)
+    if rot_dim and rot_dim != x.shape[-1]:
+        return torch.cat((apply_rope1(x_norm[..., :rot_dim], freqs_cis), x_norm[..., rot_dim:]), dim=-1)
+    return apply_rope1(x_norm, freqs_cis)
 
 
 def norm_rope(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,

@@ -113,8 +113,8 @@ def test_argument_errors_of_the_h3_entry_points(pkg):
 
 def test_reference_rope_launcher_signature(pkg):
     """launch_rms_rope_kernel keeps the reference's 46-argument list (the
-    argtypes single_qknorm_rope.py pins) and rejects what this build does not
-    take without launching anything."""
+    argtypes single_qknorm_rope.py pins) and rejects arguments outside its
+    rules without launching anything."""
     from x_minimaxh3_amd import _lib
 
     res, args = _lib.SIGNATURES["launch_rms_rope_kernel"]
@@ -127,10 +127,14 @@ def test_reference_rope_launcher_signature(pkg):
             4096, 512, 128, 1, 0, 0, 0, 0, 4096, 512, 128, 1, 0, 0, 0, 0,
             0, 256, 0, 4, 2, 1, 1, 0, 1e-6, 2, 0, 2, False, True, None]
     assert len(base) == 46
-    interleaved = list(base)
+    interleaved = list(base)       # split_half = false runs, with its own rot_dim rule
     interleaved[44] = False
+    interleaved[11] = 12           # rot_dim
     lib.launch_rms_rope_kernel(*interleaved)
-    assert b"split-half" in lib.xmh3_last_error()
+    assert b"interleaved rot_dim" in lib.xmh3_last_error()
+    interleaved[44] = True         # split-half needs rot_dim % 16
+    lib.launch_rms_rope_kernel(*interleaved)
+    assert b"multiple of 16" in lib.xmh3_last_error()
     strided = list(base)
     strided[18] = 2            # q_s3
     lib.launch_rms_rope_kernel(*strided)

@@ -1047,6 +1047,84 @@ def test_reference_named_rope_launcher(pkg, dev, hnd_out):
     assert same(out, want, "launcher output")
 
 
+def _angle_table(shape_lead, pairs, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    ang = torch.rand(*shape_lead, pairs, generator=g) * 30
+    c, sn = torch.cos(ang), torch.sin(ang)
+    return torch.stack((c, -sn, sn, c), -1).reshape(*shape_lead, pairs, 2, 2).to(dtype)
+
+
+@pytest.mark.parametrize("dtype,tdtype,D,norm,inplace", [
+    (torch.bfloat16, torch.float32, 128, True, False),
+    (torch.bfloat16, torch.float32, 96, True, True),      # 96-wide heads, in place
+    (torch.bfloat16, torch.bfloat16, 64, False, False),
+    (torch.float16, torch.float32, 128, True, True),
+    (torch.float16, torch.float16, 128, False, True),
+    (torch.float32, torch.float32, 80, True, False),
+])
+def test_interleaved_rope_bit_exact(pkg, dev, dtype, tdtype, D, norm, inplace):
+    """apply_rope1 / rms_rope1 (pairs (2i, 2i + 1), the rotation's second
+    product fused as torch's addcmul_ does) on [B, S, H, D] with a table
+    broadcast over heads, against the oracle bit for bit; q and k of
+    rms_rope_ / apply_rope_ in place, strided q (a slice of a packed qkv)."""
+    say(f"interleaved rope {dtype} table {tdtype} D={D} norm={norm} inplace={inplace}")
+    g = torch.Generator().manual_seed(D + 7 * norm)
+    B, S, H = 2, 37, 5
+    qkv = torch.randn(B, S, 3 * H, D, generator=g).to(dtype)
+    q, k = qkv[:, :, :H], qkv[:, :, H:2 * H]
+    tab = _angle_table((B, S, 1), D // 2, D, tdtype)
+    wq = (torch.rand(D, generator=g) + 0.5).to(dtype)
+    wk = (torch.rand(D, generator=g) + 0.5).to(dtype)
+    if norm:
+        wantq, wantk = cpu_ref.rms_rope1(q, tab, wq, 1e-6), cpu_ref.rms_rope1(k, tab, wk, 1e-6)
+    else:
+        wantq, wantk = cpu_ref.apply_rope1(q, tab), cpu_ref.apply_rope1(k, tab)
+    qkvd, td = qkv.to(dev), tab.to(dev)
+    qd, kd = qkvd[:, :, :H], qkvd[:, :, H:2 * H]
+    if inplace:
+        if norm:
+            pkg.rms_rope_(qd, kd, td, wq.to(dev), wk.to(dev))
+        else:
+            pkg.apply_rope_(qd, kd, td)
+        gq, gk = qd, kd
+        torch.cuda.synchronize()
+        assert same(qkvd[:, :, 2 * H:], qkv[:, :, 2 * H:], "untouched v")
+    else:
+        if norm:
+            gq, gk = pkg.rms_rope(qd, kd, td, wq.to(dev), wk.to(dev))
+        else:
+            gq, gk = pkg.apply_rope(qd, kd, td)
+        torch.cuda.synchronize()
+    assert same(gq, wantq, "q") and same(gk, wantk, "k")
+
+
+@pytest.mark.parametrize("rot", [128, 96])
+def test_reference_named_rope_launcher_interleaved(pkg, dev, rot):
+    """launch_rms_rope_kernel with split_half = false: interleaved pairs over
+    the first rot dims, norm-only tail, into a separate output."""
+    say(f"launch_rms_rope_kernel interleaved rot={rot}")
+    from x_minimaxh3_amd import _lib
+
+    g = torch.Generator().manual_seed(26 + rot)
+    T, H, D = 51, 4, 128
+    x = torch.randn(T, H, D, generator=g).to(torch.bfloat16)
+    tab = _angle_table((1, T, 1), rot // 2, rot, torch.float32)
+    w = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    xd, td, wd = x.to(dev), tab.to(dev), w.to(dev)
+    out = torch.zeros_like(xd)
+    q4, o4 = xd.unsqueeze(0), out.unsqueeze(0)
+    z4 = (0, 0, 0, 0)
+    args = ([q4.data_ptr(), None, td.data_ptr(), wd.data_ptr(), None, o4.data_ptr(), None]
+            + list(q4.shape[:3]) + [D, rot] + list(td.shape[:3])
+            + list(q4.stride()) + list(z4) + list(o4.stride()) + list(z4) + list(td.stride())
+            + [wd.stride(0), 0, 1e-6, 2, 0, 2, False, False, torch.cuda.current_stream().cuda_stream])
+    assert len(args) == 46
+    _lib.load().launch_rms_rope_kernel(*args)
+    torch.cuda.synchronize()
+    want = cpu_ref.rms_rope1(x.unsqueeze(0), tab, w, 1e-6, rot)[0]
+    assert same(out, want, "launcher output")
+
+
 def test_empty_token_batches(pkg, dev):
     """A batch of zero tokens returns empty results with the oracle's shapes
     and dtypes (no kernel is launched for an empty grid)."""

@@ -346,6 +346,40 @@ def test_rotation_identity_complex_and_norm():
     assert ((n0 - n1).abs() <= 2 ** -6 * n0 + 1e-6).all()
 
 
+def test_interleaved_rope_against_split_half_and_fma():
+    """apply_rope1 (pairs (2i, 2i+1)): with an fp32 table each output equals
+    the float64 f0*x0 rounded to fp32, plus f1*x1, rounded once (the fused
+    addcmul_), bit for bit; regrouping the pairs (de-interleave, rotate
+    split-half, re-interleave) gives the same result within one fp32
+    rounding before the final bf16 cast; an identity table returns x and
+    rms_rope1 with it returns F.rms_norm; a longer table is trimmed."""
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(1, 5, 3, 96, generator=g).to(torch.bfloat16)
+    ang = torch.rand(1, 5, 1, 48, generator=g) * 6.28
+    c, s = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -s, s, c), -1).reshape(1, 5, 1, 48, 2, 2)
+    out = cpu_ref.apply_rope1(x, tab)
+    x0, x1 = x[..., 0::2].double(), x[..., 1::2].double()
+    f = tab.double()
+    want = torch.empty(1, 5, 3, 96, dtype=torch.float64)
+    for r in range(2):
+        p = (f[..., r, 0] * x0).float().double()            # fl32(f0 * x0)
+        want[..., r::2] = (p + f[..., r, 1] * x1).float().double()   # one rounding of the sum
+    assert torch.equal(out, want.to(torch.bfloat16))
+    deint = torch.cat((x[..., 0::2], x[..., 1::2]), -1)
+    sh = cpu_ref.apply_rope_split_half1(deint, tab)
+    regroup = torch.stack((sh[..., :48], sh[..., 48:]), -1).reshape(x.shape)
+    assert (cpu_ref.bf16_ulp_diff(regroup, out) <= 1).all()
+    ident = torch.zeros(1, 5, 1, 48, 2, 2)
+    ident[..., 0, 0] = 1
+    ident[..., 1, 1] = 1
+    assert torch.equal(cpu_ref.apply_rope1(x, ident), x)
+    w = (1 + 0.1 * torch.randn(96, generator=g)).to(torch.bfloat16)
+    assert torch.equal(cpu_ref.rms_rope1(x, ident, w, 1e-6), F.rms_norm(x, (96,), weight=w, eps=1e-6))
+    longer = torch.cat((tab, tab[:, :, :1].expand(1, 5, 4, 48, 2, 2)), 2)   # dim 2 is 3 long in x
+    assert torch.equal(cpu_ref.apply_rope1(x, longer.contiguous()), cpu_ref.apply_rope1(x, tab.expand(1, 5, 3, 48, 2, 2)))
+
+
 def test_rms_rope_partial_tail_is_norm_only():
     g = torch.Generator().manual_seed(13)
     x = torch.randn(1, 5, 2, 128, generator=g).to(torch.bfloat16)

@@ -5,7 +5,8 @@ loaded by path: ``__graft_entry__.load_package()``).
 
 Ops (reference names and signatures): ``quantize_int8_rowwise``,
 ``int8_linear``, ``w4a8_int8_linear``, ``rms_adaln``,
-``apply_rope_split_half(_)``, ``rms_rope_split_half(_)``; fused hot-path ops:
+``apply_rope_split_half(_)``, ``rms_rope_split_half(_)`` and the interleaved
+``apply_rope(_)``, ``rms_rope(_)``; fused hot-path ops:
 ``norm_rope``, ``w8a8_mlp``, ``w4a8_mlp``. H3 call-site adapters live in
 ``h3``; the token-chunked / streamed MLP driver in ``driver``.
 """
@@ -15,6 +16,10 @@ from .exceptions import BackendError, BackendNotFoundError, BackendNotImplemente
 from .ops import (
     DTYPE_CODE_TO_DTYPE,
     DTYPE_TO_CODE,
+    apply_rope,
+    apply_rope1,
+    apply_rope1_,
+    apply_rope_,
     apply_rope_split_half,
     apply_rope_split_half1,
     apply_rope_split_half1_,
@@ -27,6 +32,10 @@ from .ops import (
     norm_rope,
     quantize_int8_rowwise,
     rms_adaln,
+    rms_rope,
+    rms_rope1,
+    rms_rope1_,
+    rms_rope_,
     rms_rope_split_half,
     rms_rope_split_half1,
     rms_rope_split_half1_,
@@ -40,6 +49,7 @@ from .ops import (
 from .registry import registry
 
 __all__ = [
+    "apply_rope", "apply_rope1", "apply_rope1_", "apply_rope_", "rms_rope", "rms_rope1", "rms_rope1_", "rms_rope_",
     "apply_rope_split_half", "apply_rope_split_half1", "apply_rope_split_half1_", "apply_rope_split_half_",
     "disable_backend", "enable_backend", "int8_linear", "list_backends", "mm_int8", "norm_rope",
     "quantize_int8_rowwise", "rms_adaln", "rms_rope_split_half", "rms_rope_split_half1",

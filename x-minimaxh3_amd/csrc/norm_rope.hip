@@ -90,9 +90,33 @@ __device__ __forceinline__ void rotate_pair(float a0, float a1, float f00, float
   r1 = TO::round(TF::round(TF::round(f10 * x0) + TF::round(f11 * x1)));
 }
 
+// The interleaved form (CK/backends/eager/rope.py:10-16): out = f[., 0] * x0,
+// then out.addcmul_(f[., 1], x1), which torch's CPU kernel evaluates as one
+// fused multiply-add in the table dtype (for 16-bit tables the product is
+// exact in fp32, so the fp32 fma rounded to TF is the same value).
+template <typename TF, typename TO>
+__device__ __forceinline__ void rotate_pair_fma(float a0, float a1, float f00, float f01, float f10,
+                                                float f11, float& r0, float& r1) {
+  const float x0 = TF::round(a0), x1 = TF::round(a1);  // x.to(freqs.dtype)
+  r0 = TO::round(TF::round(__builtin_fmaf(f01, x1, TF::round(f00 * x0))));
+  r1 = TO::round(TF::round(__builtin_fmaf(f11, x1, TF::round(f10 * x0))));
+}
+
 // table entries for 8 consecutive pairs: [pair][2][2] in TF
 template <typename TF>
 struct Tab8 { float f[8][4]; };
+
+// the first 4 pairs only (16 consecutive elements from idx)
+template <typename TF>
+__device__ __forceinline__ void load_tab4(const void* base, int64_t idx, Tab8<TF>& t) {
+  V8<TF> raw[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) ld8<TF>(base, idx + q * 8, raw[q]);
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t.f[p][e] = g8<TF>(raw[(p * 4 + e) >> 3], (p * 4 + e) & 7);
+}
 
 template <typename TF>
 __device__ __forceinline__ void load_tab8(const void* base, int64_t idx, Tab8<TF>& t) {
@@ -847,8 +871,12 @@ __device__ __forceinline__ void lds_tab8(const uint8_t* row, int seg, Tab8<TF>& 
 
 constexpr int HEAD_TAB_ROWS = 8, HEAD_TAB_ROW_BYTES = 1024;   // rot <= 128, fp32
 
-template <typename TX, typename TW, typename TF, bool NORM, int LPH, bool TABL>
+// SPLIT: pairs (i, i + rot/2), items of 8 at head offsets i and i + rot/2;
+// otherwise interleaved pairs (2i, 2i + 1), an item is 8 consecutive elements
+// (4 pairs) and the table rows are read directly.
+template <typename TX, typename TW, typename TF, bool NORM, int LPH, bool TABL, bool SPLIT>
 __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
+  static_assert(SPLIT || !TABL, "the LDS table staging serves the split-half layout");
   const int lane = threadIdx.x & 63;
   const int64_t head = (int64_t)blockIdx.x * (256 / LPH) + threadIdx.x / LPH;
   const int it = threadIdx.x % LPH;
@@ -860,20 +888,21 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
   const int64_t bs = (int64_t)a.divH.div((uint64_t)hd), h = hd - bs * a.H;
   const int64_t b = (int64_t)a.divS.div((uint64_t)bs), s = bs - b * a.S;
   const int half = a.rot >> 1;
-  const int pair_items = half / 8;
+  const int pair_items = SPLIT ? half / 8 : a.rot / 8;
   const int tail_items = (int)((a.D - a.rot) / 8);
   const bool is_pair = it < pair_items;
   const bool is_tail = !is_pair && it < pair_items + tail_items;
   int64_t c0 = 0, c1 = 0;
   if (is_pair) { c0 = it * 8; c1 = c0 + half; }
   else if (is_tail) { c0 = a.rot + (int64_t)(it - pair_items) * 8; }
+  const bool two = SPLIT && is_pair;          // the item's second 8 elements
   const int64_t xoff = b * a.sb + s * a.ss + h * a.sh;
   const int64_t ooff = b * a.ob + s * a.os + h * a.oh;
 
   V8<TX> v0, v1;
   if (is_pair || is_tail) {
     ld8<TX>(a.x, xoff + c0, v0);
-    if (is_pair) ld8<TX>(a.x, xoff + c1, v1);
+    if (two) ld8<TX>(a.x, xoff + c1, v1);
   }
   // the norm weight and the table do not depend on the reduction: their loads
   // go out with the row's, so the element pass waits on one memory latency
@@ -882,7 +911,7 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
   if constexpr (NORM) {
     if (is_pair || is_tail) {
       ld8<TW>(a.weight, c0, wv0);
-      if (is_pair) ld8<TW>(a.weight, c1, wv1);
+      if (two) ld8<TW>(a.weight, c1, wv1);
     }
   }
   if constexpr (TABL) {
@@ -905,8 +934,10 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     __syncthreads();
     if (is_pair && live)
       lds_tab8<TF>(tabs + (bs - bs0) * HEAD_TAB_ROW_BYTES, it, tab);
-  } else {
+  } else if constexpr (SPLIT) {
     if (is_pair) load_tab8<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 8 * 4, tab);
+  } else {
+    if (is_pair) load_tab4<TF>(a.freqs, b * a.fb + s * a.fs + h * a.fh + (int64_t)it * 4 * 4, tab);
   }
   float rr = 1.0f;
   if constexpr (NORM) {
@@ -920,7 +951,7 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     typename TX::storage* hrow = heads[threadIdx.x / LPH];
     if (is_pair || is_tail) {
       st8<TX>(hrow, c0, v0);
-      if (is_pair) st8<TX>(hrow, c1, v1);
+      if (two) st8<TX>(hrow, c1, v1);
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
@@ -998,7 +1029,18 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
     }
   };
   normalise(v0, wv0, y0);
-  if (is_pair) {
+  if constexpr (!SPLIT) {
+    if (is_pair) {
+      float r0[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        rotate_pair_fma<TF, F32T>(y0[2 * j], y0[2 * j + 1], tab.f[j][0], tab.f[j][1], tab.f[j][2], tab.f[j][3],
+                                  r0[2 * j], r0[2 * j + 1]);
+      st8<TX>(a.out, ooff + c0, pack8<TX>(r0));
+      return;
+    }
+  }
+  if (two) {
     normalise(v1, wv1, y1);
     float r0[8], r1[8];
 #pragma unroll
@@ -1227,26 +1269,26 @@ int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D,
   return fail(XMH3_EUNSUPPORTED, "rms_adaln: dtype combination not supported");
 }
 
-template <typename TX, typename TW, typename TF, bool NORM>
+template <typename TX, typename TW, typename TF, bool NORM, bool SPLIT>
 static int launch_head(HeadArgs& a, int lph, hipStream_t st) {
   const int64_t nheads = a.B * a.S * a.H;
   // table rows through LDS: shared by the heads of a token, at most
   // HEAD_TAB_ROWS tokens per block, rows of at most HEAD_TAB_ROW_BYTES
   auto tabl_ok = [&](int L) {
     const int64_t g = 256 / L;
-    return a.fh == 0 && (int64_t)(a.rot / 2) * 4 * (int64_t)sizeof(typename TF::storage) <= HEAD_TAB_ROW_BYTES &&
+    return SPLIT && a.fh == 0 && (int64_t)(a.rot / 2) * 4 * (int64_t)sizeof(typename TF::storage) <= HEAD_TAB_ROW_BYTES &&
            (g - 1) / a.H + 2 <= HEAD_TAB_ROWS;
   };
 #define XMH3_H(L)                                                                               \
   if (lph == L) {                                                                               \
     dim3 grid((unsigned)((nheads + (256 / L) - 1) / (256 / L)));                                \
-    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L, false>), grid, dim3(256), 0, st, a); \
+    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L, false, SPLIT>), grid, dim3(256), 0, st, a); \
     return check_launch("headspan_kernel");                                                     \
   }
 #define XMH3_HT(L)                                                                              \
   if (lph == L && tabl_ok(L)) {                                                                 \
     dim3 grid((unsigned)((nheads + (256 / L) - 1) / (256 / L)));                                \
-    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L, true>), grid, dim3(256), 0, st, a); \
+    hipLaunchKernelGGL((headspan_kernel<TX, TW, TF, NORM, L, SPLIT, SPLIT>), grid, dim3(256), 0, st, a); \
     return check_launch("headspan_kernel");                                                     \
   }
   XMH3_HT(4) XMH3_HT(8) XMH3_HT(16)
@@ -1259,19 +1301,23 @@ static int launch_head(HeadArgs& a, int lph, hipStream_t st) {
 int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
                const int64_t* xstrides, const int64_t* ostrides, const void* weight,
                int weight_dtype, const void* freqs, int freqs_dtype, const int64_t* fstrides,
-               int rot_dim, float eps, int norm, hipStream_t st) {
+               int rot_dim, float eps, int norm, int split_half, hipStream_t st) {
   XMH3_REQUIRE(B >= 0 && S >= 0 && H >= 0 && D > 0, "rope: bad sizes");
   if (B * S * H == 0) return XMH3_OK;
   const int rot = rot_dim ? rot_dim : (int)D;
-  XMH3_REQUIRE(rot > 0 && rot <= D && rot % 16 == 0 && (D - rot) % 8 == 0,
-               "rope: rot_dim must be a multiple of 16 and (head_dim - rot_dim) a multiple of 8");
+  if (split_half)
+    XMH3_REQUIRE(rot > 0 && rot <= D && rot % 16 == 0 && (D - rot) % 8 == 0,
+                 "rope: rot_dim must be a multiple of 16 and (head_dim - rot_dim) a multiple of 8");
+  else
+    XMH3_REQUIRE(rot > 0 && rot <= D && rot % 8 == 0 && D % 8 == 0,
+                 "rope: interleaved rot_dim and head_dim must be multiples of 8");
   XMH3_REQUIRE(x && out && freqs && (!norm || weight), "rope: null pointer");
   for (int i = 0; i < 3; ++i)
     XMH3_REQUIRE(xstrides[i] % 8 == 0 && ostrides[i] % 8 == 0 && fstrides[i] % 8 == 0,
                  "rope: strides must be multiples of 8 elements");
   XMH3_REQUIRE(aligned16(x) && aligned16(out) && aligned16(freqs) && (!weight || aligned16(weight)),
                "rope: pointers must be 16-byte aligned");
-  const int items = rot / 16 + (int)(D - rot) / 8;
+  const int items = (split_half ? rot / 16 : rot / 8) + (int)(D - rot) / 8;
   int lph = 1;
   while (lph < items) lph <<= 1;
   XMH3_REQUIRE(lph <= 64 && D <= 512, "rope: head_dim must be at most 512");
@@ -1284,11 +1330,16 @@ int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, i
   a.rot = rot; a.eps = eps;
   XMH3_REQUIRE(!norm || weight_dtype == dtype || weight_dtype == DT_F32,
                "rope: norm weight must have x's dtype or fp32");
-#define XMH3_HD(TX, TF)                                                                   \
-  {                                                                                       \
-    if (!norm) return launch_head<TX, TX, TF, false>(a, lph, st);                         \
-    if (weight_dtype == DT_F32) return launch_head<TX, F32T, TF, true>(a, lph, st);        \
-    return launch_head<TX, TX, TF, true>(a, lph, st);                                     \
+#define XMH3_HS(TX, TF, SPLIT)                                                                \
+  {                                                                                           \
+    if (!norm) return launch_head<TX, TX, TF, false, SPLIT>(a, lph, st);                      \
+    if (weight_dtype == DT_F32) return launch_head<TX, F32T, TF, true, SPLIT>(a, lph, st);     \
+    return launch_head<TX, TX, TF, true, SPLIT>(a, lph, st);                                  \
+  }
+#define XMH3_HD(TX, TF)                     \
+  {                                         \
+    if (split_half) XMH3_HS(TX, TF, true)   \
+    XMH3_HS(TX, TF, false)                  \
   }
   if (dtype == DT_BF16 && freqs_dtype == DT_F32) XMH3_HD(BF16T, F32T)
   if (dtype == DT_BF16 && freqs_dtype == DT_BF16) XMH3_HD(BF16T, BF16T)
@@ -1296,6 +1347,7 @@ int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, i
   if (dtype == DT_F16 && freqs_dtype == DT_F16) XMH3_HD(F16T, F16T)
   if (dtype == DT_F32 && freqs_dtype == DT_F32) XMH3_HD(F32T, F32T)
 #undef XMH3_HD
+#undef XMH3_HS
   return fail(XMH3_EUNSUPPORTED, "rope: dtype combination not supported");
 }
 
@@ -1327,9 +1379,9 @@ extern "C" int xmh3_rms_adaln(const void* x, void* out, int dtype, int64_t rows,
 // The reference's 46-argument launcher, same name and argument list, so a
 // ctypes caller with pinned argtypes binds this library unchanged. It returns
 // nothing, as the reference's does: an argument this build does not take
-// (interleaved pairs, a non-contiguous last dimension, a strided weight or
-// table pair layout) launches nothing and leaves the message in
-// xmh3_last_error(). Size-1 table dimensions broadcast.
+// (a non-contiguous last dimension, a strided weight or table pair layout)
+// launches nothing and leaves the message in xmh3_last_error(). Both pair
+// layouts (split_half true or false) run; size-1 table dimensions broadcast.
 extern "C" void launch_rms_rope_kernel(
     const void* q, const void* k, const void* freqs, const void* q_scale, const void* k_scale, void* q_out,
     void* k_out, int64_t batch, int64_t dim1, int64_t dim2, int64_t head_dim, int64_t rot_dim,
@@ -1341,7 +1393,6 @@ extern "C" void launch_rms_rope_kernel(
     bool split_half, hipStream_t stream) {
   using namespace xmh3;
   auto reject = [](const char* msg) { fail(XMH3_EUNSUPPORTED, msg); };
-  if (!split_half) return reject("launch_rms_rope_kernel: only the split-half pair layout is supported");
   if (q_s3 != 1 || qo_s3 != 1 || (has_k && (k_s3 != 1 || ko_s3 != 1)))
     return reject("launch_rms_rope_kernel: the head dimension must be contiguous");
   if (f_s5 != 1 || f_s4 != 2 || f_s3 != 4)
@@ -1356,14 +1407,15 @@ extern "C" void launch_rms_rope_kernel(
   {
     const int64_t xs[3] = {q_s0, q_s1, q_s2}, os[3] = {qo_s0, qo_s1, qo_s2};
     if (rope_heads(const_cast<void*>(q), q_out, input_dtype_code, batch, dim1, dim2, head_dim, xs, os, q_scale,
-                   scale_dtype_code, freqs, freqs_dtype_code, fst, (int)rot_dim, epsilon, norm, stream) != XMH3_OK)
+                   scale_dtype_code, freqs, freqs_dtype_code, fst, (int)rot_dim, epsilon, norm, split_half,
+                   stream) != XMH3_OK)
       return;
   }
   if (has_k) {
     const int64_t xs[3] = {k_s0, k_s1, k_s2}, os[3] = {ko_s0, ko_s1, ko_s2};
     rope_heads(const_cast<void*>(k), k_out, input_dtype_code, batch, dim1, dim2, head_dim, xs, os,
                k_scale ? k_scale : q_scale, scale_dtype_code, freqs, freqs_dtype_code, fst, (int)rot_dim, epsilon,
-               k_scale ? 1 : norm, stream);
+               k_scale ? 1 : norm, split_half, stream);
   }
 }
 
@@ -1374,6 +1426,15 @@ extern "C" int xmh3_rope_split_half(void* x, void* out, int dtype, int64_t B, in
                                     const int64_t* freqs_strides, int rot_dim, float eps, int norm,
                                     hipStream_t stream) {
   return xmh3::rope_heads(x, out, dtype, B, S, H, head_dim, x_strides, out_strides, norm_weight,
-                          weight_dtype, freqs, freqs_dtype, freqs_strides, rot_dim, eps, norm,
+                          weight_dtype, freqs, freqs_dtype, freqs_strides, rot_dim, eps, norm, 1,
+                          stream);
+}
+
+extern "C" int xmh3_rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t head_dim,
+                               const int64_t* x_strides, const int64_t* out_strides, const void* norm_weight,
+                               int weight_dtype, const void* freqs, int freqs_dtype, const int64_t* freqs_strides,
+                               int rot_dim, float eps, int norm, int split_half, hipStream_t stream) {
+  return xmh3::rope_heads(x, out, dtype, B, S, H, head_dim, x_strides, out_strides, norm_weight,
+                          weight_dtype, freqs, freqs_dtype, freqs_strides, rot_dim, eps, norm, split_half,
                           stream);
 }

@@ -13,6 +13,8 @@ backends/turbo/vendor/comfy_kitchen):
   rms_adaln               CK/__init__.py:130-150
   apply_rope_split_half(_), apply_rope_split_half1(_)   CK/__init__.py:629-690
   rms_rope_split_half(_), rms_rope_split_half1(_)        CK/__init__.py:549-603
+  apply_rope(_), apply_rope1(_), rms_rope(_), rms_rope1(_) (interleaved pairs)
+                          CK/backends/eager/rope.py:10-36,95-166
 
 plus the fused entries of the hot path: ``norm_rope``, ``w8a8_mlp``,
 ``w4a8_mlp``.
@@ -240,6 +242,48 @@ def rms_rope_split_half1(x, freqs_cis, scale, epsilon: float = 1e-6):
 def rms_rope_split_half1_(x, freqs_cis, scale, epsilon: float = 1e-6):
     kw = {"x": x, "freqs_cis": freqs_cis, "scale": scale, "epsilon": epsilon}
     return _impl("rms_rope_split_half1_", kw)(**kw)
+
+
+def apply_rope(xq: torch.Tensor, xk: torch.Tensor, freqs_cis: torch.Tensor):
+    """RoPE on interleaved pairs (2i, 2i + 1) of q and k."""
+    kw = {"xq": xq, "xk": xk, "freqs_cis": freqs_cis}
+    return _impl("apply_rope", kw)(**kw)
+
+
+def apply_rope_(xq: torch.Tensor, xk: torch.Tensor, freqs_cis: torch.Tensor):
+    kw = {"xq": xq, "xk": xk, "freqs_cis": freqs_cis}
+    return _impl("apply_rope_", kw)(**kw)
+
+
+def apply_rope1(x: torch.Tensor, freqs_cis: torch.Tensor) -> torch.Tensor:
+    kw = {"x": x, "freqs_cis": freqs_cis}
+    return _impl("apply_rope1", kw)(**kw)
+
+
+def apply_rope1_(x: torch.Tensor, freqs_cis: torch.Tensor) -> torch.Tensor:
+    kw = {"x": x, "freqs_cis": freqs_cis}
+    return _impl("apply_rope1_", kw)(**kw)
+
+
+def rms_rope(q, k, freqs_cis, q_scale, k_scale=None, epsilon: float = 1e-6):
+    """Per-head RMSNorm with weight + RoPE on interleaved pairs."""
+    kw = {"q": q, "k": k, "freqs_cis": freqs_cis, "q_scale": q_scale, "k_scale": k_scale, "epsilon": epsilon}
+    return _impl("rms_rope", kw)(**kw)
+
+
+def rms_rope_(q, k, freqs_cis, q_scale, k_scale=None, epsilon: float = 1e-6):
+    kw = {"q": q, "k": k, "freqs_cis": freqs_cis, "q_scale": q_scale, "k_scale": k_scale, "epsilon": epsilon}
+    return _impl("rms_rope_", kw)(**kw)
+
+
+def rms_rope1(x, freqs_cis, scale, epsilon: float = 1e-6):
+    kw = {"x": x, "freqs_cis": freqs_cis, "scale": scale, "epsilon": epsilon}
+    return _impl("rms_rope1", kw)(**kw)
+
+
+def rms_rope1_(x, freqs_cis, scale, epsilon: float = 1e-6):
+    kw = {"x": x, "freqs_cis": freqs_cis, "scale": scale, "epsilon": epsilon}
+    return _impl("rms_rope1_", kw)(**kw)
 
 
 def norm_rope(q: torch.Tensor, k: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
