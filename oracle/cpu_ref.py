@@ -546,6 +546,31 @@ def rms_rope1(x: torch.Tensor, freqs_cis: torch.Tensor, weight: torch.Tensor, ep
     return apply_rope1(x_norm, freqs_cis)
 
 
+def qknorm_rope_angles(value: torch.Tensor, weight: torch.Tensor, angles: torch.Tensor, eps: float,
+                       cos_sin: tuple | None = None) -> torch.Tensor:
+    """The angle-table branch of H3's apply_qknorm_rope
+    (h3serve/native_engine/model/layers.py:126-149) for one of q or k:
+    F.rms_norm with the weight in the value dtype, then active * cos +
+    cat(-second, first) * sin in the value dtype over the first rot =
+    angles.shape[-1] dims, cos and sin of the first half of the angles cast to
+    the value dtype. ``cos_sin`` replaces those two tables (for checking a
+    device-computed table)."""
+    value = F.rms_norm(value, (value.shape[-1],), weight=weight.to(dtype=value.dtype), eps=eps)
+    rot = int(angles.shape[-1])
+    half = rot // 2
+    if cos_sin is None:
+        cosine = torch.cos(angles[:, :half]).to(value.dtype)
+        sine = torch.sin(angles[:, :half]).to(value.dtype)
+    else:
+        cosine, sine = (t.to(value.dtype) for t in cos_sin)
+    cosine = torch.cat((cosine, cosine), dim=-1).unsqueeze(1)
+    sine = torch.cat((sine, sine), dim=-1).unsqueeze(1)
+    active, passthrough = value[..., :rot], value[..., rot:]
+    first, second = active.chunk(2, dim=-1)
+    perpendicular = torch.cat((-second, first), dim=-1)
+    return torch.cat((active * cosine + perpendicular * sine, passthrough), dim=-1)
+
+
 def norm_rope(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
               freqs_cis: torch.Tensor, head_dim: int = 128, eps: float = 1e-6) -> torch.Tensor:
     """The fused AdaLN-RMSNorm + 3D RoPE composite for one of Q or K:

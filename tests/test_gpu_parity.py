@@ -619,6 +619,40 @@ def test_h3_qknorm_rope_partial_inplace(pkg, dev):
     assert torch.equal(out[:, :, 2], qkv[:, :, 2])    # v untouched
 
 
+def test_h3_qknorm_rope_angle_form(pkg, dev):
+    """H3's apply_qknorm_rope with [S, rot] angles (96 of 128): the table the
+    device builds (torch's cos / sin on the GPU, rounded to bf16) is within
+    one bf16 step of the CPU's; given that table, q and k equal the oracle
+    restatement of the reference's angle branch bit for bit; the inputs are
+    left unchanged (the branch returns new tensors)."""
+    say("apply_qknorm_rope angle form rot 96 of 128")
+    from x_minimaxh3_amd import h3
+
+    g = torch.Generator().manual_seed(27)
+    S, H, D, rot = 299, 6, 128, 96
+    q = torch.randn(S, H, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(S, H, D, generator=g).to(torch.bfloat16)
+    qw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    half = torch.rand(S, rot // 2, generator=g) * 60
+    angles = torch.cat((half, half), -1)
+    qd, kd = q.to(dev), k.to(dev)
+    oq, ok = h3.apply_qknorm_rope(qd, kd, q_weight=qw.to(dev), k_weight=kw.to(dev), frequencies=angles.to(dev),
+                                  eps=1e-5)
+    tab = h3.angle_rotation_table(angles.to(dev), torch.bfloat16).cpu()
+    torch.cuda.synchronize()
+    c_dev, s_dev = tab[0, :, 0, :, 0, 0], tab[0, :, 0, :, 1, 0]
+    c_cpu, s_cpu = torch.cos(half).to(torch.bfloat16), torch.sin(half).to(torch.bfloat16)
+    assert (cpu_ref.bf16_ulp_diff(c_dev, c_cpu) <= 1).all() and (cpu_ref.bf16_ulp_diff(s_dev, s_cpu) <= 1).all()
+    say(f"  device cos/sin differ from the CPU's at {(c_dev != c_cpu).sum().item() + (s_dev != s_cpu).sum().item()}"
+        f" of {2 * c_cpu.numel()} entries")
+    assert torch.equal(tab[0, :, 0, :, 0, 1], -s_dev) and torch.equal(tab[0, :, 0, :, 1, 1], c_dev)
+    wq = cpu_ref.qknorm_rope_angles(q, qw, angles, 1e-5, cos_sin=(c_dev, s_dev))
+    wk = cpu_ref.qknorm_rope_angles(k, kw, angles, 1e-5, cos_sin=(c_dev, s_dev))
+    assert same(oq, wq, "q") and same(ok, wk, "k")
+    assert same(qd, q, "q input") and same(kd, k, "k input")
+
+
 @pytest.mark.parametrize("mod_dtype", [torch.bfloat16, torch.float32])
 def test_rms_adaln(pkg, dev, mod_dtype):
     say(f"rms_adaln scale/shift {mod_dtype}")

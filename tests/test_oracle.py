@@ -380,6 +380,28 @@ def test_interleaved_rope_against_split_half_and_fma():
     assert torch.equal(cpu_ref.apply_rope1(x, longer.contiguous()), cpu_ref.apply_rope1(x, tab.expand(1, 5, 3, 48, 2, 2)))
 
 
+def test_angle_form_qknorm_rope_equals_the_table_form():
+    """H3's angle-table branch (active * cos + (-second, first) * sin in the
+    value dtype) equals the split-half table form with the table (cos, -sin,
+    sin, cos) in the value dtype, bit for bit, partial rotation and
+    pass-through tail included; and with an fp32 table it differs (the
+    rounding point of the table matters)."""
+    g = torch.Generator().manual_seed(15)
+    S, H, D, rot = 41, 3, 128, 96
+    x = torch.randn(S, H, D, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16)
+    half_angles = torch.rand(S, rot // 2, generator=g) * 40
+    angles = torch.cat((half_angles, half_angles), -1)
+    want = cpu_ref.qknorm_rope_angles(x, w, angles, 1e-5)
+    c, s = torch.cos(half_angles), torch.sin(half_angles)
+    tab16 = torch.stack((c, -s, s, c), -1).reshape(1, S, 1, rot // 2, 2, 2).to(torch.bfloat16)
+    got = cpu_ref.rms_rope_split_half1(x.unsqueeze(0), tab16, w, 1e-5, rot)[0]
+    assert torch.equal(got, want)
+    tab32 = torch.stack((c, -s, s, c), -1).reshape(1, S, 1, rot // 2, 2, 2)
+    assert not torch.equal(cpu_ref.rms_rope_split_half1(x.unsqueeze(0), tab32, w, 1e-5, rot)[0], want)
+    assert torch.equal(want[..., rot:], F.rms_norm(x, (D,), weight=w, eps=1e-5)[..., rot:])
+
+
 def test_rms_rope_partial_tail_is_norm_only():
     g = torch.Generator().manual_seed(13)
     x = torch.randn(1, 5, 2, 128, generator=g).to(torch.bfloat16)

@@ -85,12 +85,37 @@ def rms_adaln(value: torch.Tensor, norm, shift: torch.Tensor, scale: torch.Tenso
     return backend.rms_adaln_rows(value, weight, scale.to(value.dtype), shift.to(value.dtype), row_map, eps)
 
 
+def angle_rotation_table(angles: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """[S, rot] split-half angles -> the packed [1, S, 1, rot/2, 2, 2] table
+    (cos, -sin, sin, cos) of their first half in ``dtype``, computed where
+    the angles are (H3/layers.py:61-69)."""
+    half = angles.shape[-1] // 2
+    active = angles[:, :half]
+    c, s = torch.cos(active), torch.sin(active)
+    return torch.stack((c, -s, s, c), dim=-1).reshape(1, angles.shape[0], 1, half, 2, 2).to(dtype)
+
+
 def apply_qknorm_rope(query: torch.Tensor, key: torch.Tensor, *, q_weight: torch.Tensor, k_weight: torch.Tensor,
                       frequencies: torch.Tensor, eps: float):
-    """Per-head RMSNorm then split-half partial RoPE, in place, for the packed
-    [1, S, 1, rot/2, 2, 2] table form."""
+    """Per-head RMSNorm then split-half partial RoPE (H3/layers.py:72-149).
+
+    The packed [1, S, 1, rot/2, 2, 2] table form runs in place, as the
+    reference's GPU branch does. The angle form ([S, rot] angles) returns new
+    tensors, as the reference does: its rotation active * cos + (-second,
+    first) * sin in the value dtype, with cos and sin of the first half of
+    the angles rounded to that dtype, is the table form with the table
+    (cos, -sin, sin, cos) in the value dtype, so it runs the same kernel on
+    ``angle_rotation_table(angles, query.dtype)``."""
     if frequencies.ndim != 6:
-        raise NotImplementedError("the angle-table form of apply_qknorm_rope is not implemented")
+        if frequencies.ndim != 2:
+            raise ValueError(f"frequencies must be a packed 6-D table or [S, rot] angles, got {tuple(frequencies.shape)}")
+        rot = int(frequencies.shape[-1])
+        table = angle_rotation_table(frequencies.to(query.device), query.dtype)
+        q_out, k_out = ops.rms_rope_split_half(query.unsqueeze(0), key.unsqueeze(0), table,
+                                               q_weight.to(device=query.device, dtype=query.dtype),
+                                               k_weight.to(device=key.device, dtype=key.dtype), epsilon=eps,
+                                               rot_dim=rot)
+        return q_out[0], k_out[0]
     rot = int(frequencies.shape[-3]) * 2
     q4, k4 = query.unsqueeze(0), key.unsqueeze(0)
     ops.rms_rope_split_half_(q4, k4, frequencies, q_weight.to(device=query.device, dtype=query.dtype),
