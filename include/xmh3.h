@@ -76,11 +76,12 @@ int xmh3_quantize_int8_rowwise_ex(const void* x, int x_dtype, int input_act, int
  * Per-token int8 quantisation of a rotated linear's input:
  *   a = act(x)  (input_act 0 none, 1 gelu_tanh, 2 swiglu: x rows are
  *               [gate | up], 2*K wide, a = T(T(silu(gate)) * up))
- *   r = T(a_g @ H) per group of 256 columns (H = H4 (x) H4 (x) H4 (x) H4 / 16)
+ *   r = T(a_g @ H) per group of G = 4^n columns (H = H4 (x) ... (x) H4 / 2^n)
  *   (q, scale) = quantize_int8_rowwise(r)
- * group_size 256 (the only ConvRot group the fused path takes) or 0 (no
- * rotation; then input_act must be 2). K (the activated width) % 256 == 0,
- * K <= 16384; x rows 16-byte aligned (ldx % 8 == 0); x bf16 or fp16.
+ * group_size G in {4, 16, 64, 256, 1024} (the reference's fused kernel takes
+ * 256, its eager path any power of 4) or 0 (no rotation; then input_act must
+ * be 2). K (the activated width) % 256 == 0 and % G == 0, K <= 16384; x rows
+ * 16-byte aligned (ldx % 8 == 0); x bf16 or fp16.
  * q: int8 [M, K] contiguous; scale: fp32 [M].
  * Replaces: CK/backends/cuda/ops/int8_linear.cu:1295
  *   launch_quantize_int8_rowwise_convrot64_kernel(input, output, scales, rows,

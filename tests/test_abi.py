@@ -85,8 +85,11 @@ def test_argument_errors_of_the_h3_entry_points(pkg):
     fake = 4096   # aligned, never used
     err = lambda: lib.xmh3_last_error()
     # ConvRot quantizer: group, width, activation
-    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 256, 256, 64, fake, fake, None) == 1
-    assert b"convrot_groupsize" in err()
+    for bad_group in (32, 2048, 4096, 3):
+        assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 4096, 4096, bad_group, fake, fake, None) == 1
+        assert b"convrot_groupsize" in err()
+    assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 768, 768, 1024, fake, fake, None) == 1
+    assert b"multiple of convrot_groupsize" in err()
     assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 100, 128, 256, fake, fake, None) == 1
     assert b"multiple of 256" in err()
     assert lib.xmh3_quantize_int8_rowwise_convrot(fake, 2, 0, 4, 16640, 16640, 256, fake, fake, None) == 1

@@ -42,8 +42,10 @@ def test_unimplemented_reference_features_raise(pkg):
 
     x = torch.randn(2, 256).bfloat16()
     w = torch.zeros(8, 256, dtype=torch.int8)
-    with pytest.raises(NotImplementedError, match="ConvRot group size 64"):
-        backend.int8_linear(x, w, torch.ones(8), convrot=True, convrot_groupsize=64)
+    with pytest.raises(NotImplementedError, match="ConvRot group size 4096"):
+        backend.int8_linear(x, w, torch.ones(8), convrot=True, convrot_groupsize=4096)
+    with pytest.raises(NotImplementedError, match="multiple of the ConvRot group size 1024"):
+        backend.int8_linear(x, w, torch.ones(8), convrot=True, convrot_groupsize=1024)
     with pytest.raises(NotImplementedError, match="activated width 128"):
         backend.int8_linear(x, w[:, :128].contiguous(), torch.ones(8), input_act="swiglu")
     with pytest.raises(NotImplementedError, match="dtype"):

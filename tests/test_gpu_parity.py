@@ -840,6 +840,39 @@ def test_convrot_quantizer_exact_rows(pkg, dev):
     assert same(qv, qr, "strided codes") and same(sv, sr, "strided scales")
 
 
+@pytest.mark.parametrize("group", [4, 16, 64, 1024])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_convrot_quantizer_group_sizes(pkg, dev, group, dtype):
+    """ConvRot groups other than 256 (the eager path takes any power of 4):
+    integer rows (every partial sum exact, so any summation order agrees)
+    are bit-exact with the oracle, a spike spreads over exactly its own
+    group; N(0, 1) rows with outliers, with GELU, meet the code-mismatch bar
+    of the 256 case."""
+    say(f"convrot quantizer group {group} {dtype}")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(group)
+    m, k = 45, 3072 if group < 1024 else 4096
+    x = torch.randint(-30, 31, (m, k), generator=g).float()
+    x[7] = 0.0
+    x[7, 1000] = 500.0
+    x = x.to(dtype)
+    q, s = backend.quantize_int8_rowwise_convrot64(x.to(dev), group)
+    torch.cuda.synchronize()
+    qr, sr, _ = cpu_ref.quantize_convrot(x, group, None)
+    assert same(q, qr, "exact-row codes") and same(s, sr, "exact-row scales")
+    lo = 1000 // group * group
+    nz = (q[7].cpu() != 0).nonzero().flatten()
+    assert nz.min().item() >= lo and nz.max().item() < lo + group and nz.numel() == group
+    xo = (outlier_acts(m, k, seed=group + 1) * 0.5).to(dtype)
+    q2, s2 = backend.quantize_int8_rowwise_convrot64(xo.to(dev), group, input_act="gelu_tanh")
+    torch.cuda.synchronize()
+    qr2, sr2, _ = cpu_ref.quantize_convrot(xo, group, "gelu_tanh")
+    assert torch.allclose(s2.cpu(), sr2, rtol=2 ** -7, atol=0)
+    mism, dq = _code_stats(q2, qr2, f"group {group} codes")
+    assert mism < 2e-3 and dq <= 1
+
+
 @pytest.mark.parametrize("act", [None, "gelu_tanh", "swiglu"])
 def test_convrot_quantizer_fp16(pkg, dev, act):
     say(f"convrot quantizer, fp16 rows, act={act}")

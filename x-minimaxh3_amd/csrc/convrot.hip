@@ -7,31 +7,35 @@
 //   a = act(x)        CK/backends/_activations.py:40-53, in x's dtype:
 //                     gelu_tanh -> T(gelu(x)); swiglu on [gate | up] rows ->
 //                     T(T(silu(gate)) * up), the row halving in width
-//   r = T(a_g @ H)    per group g of 256 columns, H the normalised regular
-//                     Hadamard matrix H4 (x) H4 (x) H4 (x) H4 / 16
-//                     (CK/tensor/int8_utils.py:11-74,
+//   r = T(a_g @ H)    per group g of G = 4^n columns (n = 1..5), H the
+//                     normalised regular Hadamard matrix H4 (x) ... (x) H4
+//                     (n factors) / 2^n (CK/tensor/int8_utils.py:11-74,
 //                     CK/backends/eager/quantization.py:1012-1017)
 //   (q, s) = quantize_int8_rowwise(r)   as in quant.hip
-// The rotation is evaluated in fp32 as four radix-4 stages (one per base-4
+// The rotation is evaluated in fp32 as n radix-4 stages (one per base-4
 // digit of the column inside its group; H4 is symmetric and
 // H4[i][j] = -1 exactly when i + j == 3, so a stage output is
 // sum(a_0..a_3) - 2 * a_(3-j)), then rounded to T once. The reference's fp32
 // accumulation order inside its bf16 matmul is a library detail; every order
 // gives the same fp32 sums when they are exact (a group whose values span at
 // most about 8 binades), otherwise the last bit of r may differ. The stages
-// sum without the 1/16 (up to 256 |a|), so activations beyond 2^120 in
+// sum without the 1/2^n (up to G |a|), so activations beyond 2^117 in
 // magnitude overflow here where the normalised matmul would still be finite.
 //
 // Layout: one block per row, W waves (W * NIT * 4 >= K / 256). In iteration
-// it, wave w takes the four groups 4 * (it * W + w) .. +3, one per 16-lane
-// row of the wave; lane l of a row holds the 16 consecutive columns
-// 16 * l .. +15 of its group (digits 0 and 1 of the column inside the lane,
-// digit 2 in lane bits 0-1, digit 3 in lane bits 2-3). The cross-lane stages
-// use DPP (quad permutes and 16-lane row rotations) and leave each lane with
-// the outputs of the mirrored lane 15 - l, so lane l stores its codes at
-// 16 * (15 - l). The rotated row stays in registers (fp32 for bf16, packed
-// 16-bit for fp16) until the block knows its |max|. With group size 0 the same kernel quantizes the
-// swiglu activation without a rotation.
+// it, wave w takes the four 256-column chunks 4 * (it * W + w) .. +3, one
+// per 16-lane row of the wave; lane l of a row holds the 16 consecutive
+// columns 16 * l .. +15 of its chunk. Base-4 digits 0 and 1 of a column are
+// inside the lane, digit 2 in lane bits 0-1, digit 3 in lane bits 2-3,
+// digit 4 in lane bits 4-5 (the row): a group of G columns is the run of
+// those digits below n. The quad and half-row stages use DPP (quad permutes
+// and 16-lane row rotations) and leave each lane with the outputs of the
+// lane whose digit is mirrored (3 - d), so lane l stores its codes at slot
+// l ^ 3 (n = 3) or l ^ 15 (n >= 4); the row stage (G = 1024) goes through
+// lane shuffles and is not mirrored. The rotated row stays in registers
+// (fp32 for bf16, packed 16-bit for fp16) until the block knows its |max|.
+// With group size 0 the same kernel quantizes the swiglu activation
+// without a rotation.
 #include "common.hpp"
 
 #include <type_traits>
@@ -60,6 +64,14 @@ __device__ __forceinline__ float h4_lanes_mirrored(float a) {
   return __builtin_fmaf(a, -2.0f, s);
 }
 
+// radix-4 stage across the four 16-lane rows of the wave (digit 4, lane bits
+// 4-5): row j gets (sum of the four) - 2 * (row 3 - j) = lane ^ 48
+__device__ __forceinline__ float h4_rows(float a) {
+  const float t = a + __shfl_xor(a, 16, 64);
+  const float s = t + __shfl_xor(t, 32, 64);
+  return __builtin_fmaf(__shfl_xor(a, 48, 64), -2.0f, s);
+}
+
 // in-lane radix-4 stage over 4 values: b_j = (a0 + a1 + a2 + a3) - 2 a_(3-j)
 __device__ __forceinline__ void h4_inlane(float& a0, float& a1, float& a2, float& a3) {
   const float s = (a0 + a1) + (a2 + a3);
@@ -83,7 +95,8 @@ __device__ __forceinline__ float cr_act_swiglu(float g, float u) {
 
 typedef uint32_t cr_u32x4 __attribute__((ext_vector_type(4)));
 
-template <typename T, int ACT, bool ROT, int NIT>
+// LOGG: radix-4 stages n (group 4^n), 0 = no rotation
+template <typename T, int ACT, int LOGG, int NIT>
 __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
     const typename T::storage* __restrict__ x, int64_t ldx, int K, int8_t* __restrict__ q, int64_t ldq,
     float* __restrict__ scale) {
@@ -135,18 +148,21 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
         v[i] = xi;
       }
     }
-    if constexpr (ROT) {
+    if constexpr (LOGG >= 1) {
       // digit 0 (i & 3) and digit 1 (i >> 2), inside the lane
 #pragma unroll
       for (int d1 = 0; d1 < 4; ++d1) h4_inlane(v[4 * d1], v[4 * d1 + 1], v[4 * d1 + 2], v[4 * d1 + 3]);
+      if constexpr (LOGG >= 2) {
 #pragma unroll
-      for (int d0 = 0; d0 < 4; ++d0) h4_inlane(v[d0], v[4 + d0], v[8 + d0], v[12 + d0]);
-      // digit 2 (lane bits 0-1), then digit 3 (lane bits 2-3), across lanes
+        for (int d0 = 0; d0 < 4; ++d0) h4_inlane(v[d0], v[4 + d0], v[8 + d0], v[12 + d0]);
+      }
+      // digit 2 (lane bits 0-1), digit 3 (lane bits 2-3), digit 4 (the row)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        v[i] = h4_lanes_mirrored<DPP_QUAD_XOR1, DPP_QUAD_XOR2>(v[i]);
-        v[i] = h4_lanes_mirrored<DPP_ROW_ROR8, DPP_ROW_ROR4>(v[i]);
-        if constexpr (!FOLD) v[i] *= 0.0625f;   // H / 16 (exact)
+        if constexpr (LOGG >= 3) v[i] = h4_lanes_mirrored<DPP_QUAD_XOR1, DPP_QUAD_XOR2>(v[i]);
+        if constexpr (LOGG >= 4) v[i] = h4_lanes_mirrored<DPP_ROW_ROR8, DPP_ROW_ROR4>(v[i]);
+        if constexpr (LOGG >= 5) v[i] = h4_rows(v[i]);
+        if constexpr (!FOLD) v[i] *= 1.0f / (float)(1 << LOGG);   // H / 2^n (exact)
       }
     }
     // |max| of the unrounded values (lanes past the last group hold zeros):
@@ -169,7 +185,7 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
     amax = wave_amax[0];
     for (int w = 1; w < nwaves; ++w) amax = fmaxf(amax, wave_amax[w]);
   }
-  constexpr float unfold = (FOLD && ROT) ? 0.0625f : 1.0f;
+  constexpr float unfold = FOLD ? 1.0f / (float)(1 << LOGG) : 1.0f;
   const float s = fmaxf(amax * unfold / 127.0f, 1e-30f);
   float sT = T::round(s);
   if (sT == 0.0f) sT = T::tiny();
@@ -208,13 +224,14 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
         w[k] = word;
       }
     }
-    const int slot = ROT ? 15 - g16 : g16;
+    constexpr int mirror = (LOGG >= 3 ? 3 : 0) | (LOGG >= 4 ? 12 : 0);
+    const int slot = g16 ^ mirror;
     *reinterpret_cast<uint4*>(qr + group * 256 + slot * 16) = make_uint4(w[0], w[1], w[2], w[3]);
   }
   if (threadIdx.x == 0) scale[row] = s;
 }
 
-template <typename T, int ACT, bool ROT>
+template <typename T, int ACT, int LOGG>
 static int launch_convrot_T(const void* x, int64_t ldx, int64_t M, int K, int8_t* q, int64_t ldq, float* scale,
                             hipStream_t st) {
   using S = typename T::storage;
@@ -225,43 +242,59 @@ static int launch_convrot_T(const void* x, int64_t ldx, int64_t M, int K, int8_t
   if (M > 0x7fffffff) return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: more than 2^31-1 rows");
   const dim3 grid((unsigned)M), block((unsigned)(64 * waves));
   if (nit == 1)
-    hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, ROT, 1>), grid, block, 0, st, static_cast<const S*>(x),
+    hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, LOGG, 1>), grid, block, 0, st, static_cast<const S*>(x),
                        ldx, K, q, ldq, scale);
   else
-    hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, ROT, 2>), grid, block, 0, st, static_cast<const S*>(x),
+    hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, LOGG, 2>), grid, block, 0, st, static_cast<const S*>(x),
                        ldx, K, q, ldq, scale);
   return check_launch("convrot_quant_rows_kernel");
+}
+
+template <typename T, int ACT>
+static int launch_convrot_g(const void* x, int64_t ldx, int64_t M, int K, int8_t* q, int64_t ldq, float* scale,
+                            int logg, hipStream_t st) {
+  switch (logg) {
+    case 1: return launch_convrot_T<T, ACT, 1>(x, ldx, M, K, q, ldq, scale, st);
+    case 2: return launch_convrot_T<T, ACT, 2>(x, ldx, M, K, q, ldq, scale, st);
+    case 3: return launch_convrot_T<T, ACT, 3>(x, ldx, M, K, q, ldq, scale, st);
+    case 4: return launch_convrot_T<T, ACT, 4>(x, ldx, M, K, q, ldq, scale, st);
+    case 5: return launch_convrot_T<T, ACT, 5>(x, ldx, M, K, q, ldq, scale, st);
+    default: return fail(XMH3_EINVAL, "quantize_int8_rowwise_convrot: bad group size");
+  }
+}
+
+template <typename T>
+static int launch_convrot_act(const void* x, int64_t ldx, int64_t M, int K, int8_t* q, int64_t ldq, float* scale,
+                              int input_act, int logg, hipStream_t st) {
+  if (logg == 0) return launch_convrot_T<T, ACT_SWIGLU, 0>(x, ldx, M, K, q, ldq, scale, st);
+  if (input_act == ACT_SWIGLU) return launch_convrot_g<T, ACT_SWIGLU>(x, ldx, M, K, q, ldq, scale, logg, st);
+  if (input_act == ACT_GELU_TANH) return launch_convrot_g<T, ACT_GELU_TANH>(x, ldx, M, K, q, ldq, scale, logg, st);
+  return launch_convrot_g<T, ACT_NONE>(x, ldx, M, K, q, ldq, scale, logg, st);
 }
 
 int quantize_rows_convrot(const void* x, int x_dtype, int input_act, int64_t M, int64_t K, int64_t ldx,
                           int group_size, int8_t* q, int64_t ldq, float* scale, hipStream_t st) {
   XMH3_REQUIRE(M >= 0 && K >= 0, "quantize_int8_rowwise_convrot: negative size");
-  XMH3_REQUIRE(group_size == 256 || group_size == 0,
-               "quantize_int8_rowwise_convrot: convrot_groupsize must be 256 (or 0: no rotation)");
+  int logg = 0;
+  while (logg < 6 && (1 << (2 * logg)) < group_size) ++logg;
+  XMH3_REQUIRE(group_size == 0 || (logg >= 1 && logg <= 5 && (1 << (2 * logg)) == group_size),
+               "quantize_int8_rowwise_convrot: convrot_groupsize must be 4, 16, 64, 256 or 1024 (or 0: no rotation)");
   XMH3_REQUIRE(input_act == ACT_NONE || input_act == ACT_GELU_TANH || input_act == ACT_SWIGLU,
                "quantize_int8_rowwise_convrot: unsupported input activation");
   if (M == 0 || K == 0) return XMH3_OK;
   XMH3_REQUIRE(x && q && scale, "quantize_int8_rowwise_convrot: null pointer");
   XMH3_REQUIRE(K % 256 == 0 && K <= 16384, "quantize_int8_rowwise_convrot: K must be a multiple of 256, <= 16384");
+  XMH3_REQUIRE(group_size == 0 || K % group_size == 0,
+               "quantize_int8_rowwise_convrot: K must be a multiple of convrot_groupsize");
   const int64_t in_width = input_act == ACT_SWIGLU ? 2 * K : K;
   XMH3_REQUIRE(ldx >= in_width && ldx % 8 == 0 && (uintptr_t)x % 16 == 0 && ldq >= K && ldq % 16 == 0 &&
                    (uintptr_t)q % 16 == 0,
                "quantize_int8_rowwise_convrot: rows must be 16-byte aligned");
   const int k = (int)K;
-#define XMH3_CRA(TT)                                                                                    \
-  {                                                                                                     \
-    if (group_size == 0) {                                                                              \
-      if (input_act == ACT_SWIGLU) return launch_convrot_T<TT, ACT_SWIGLU, false>(x, ldx, M, k, q, ldq, scale, st); \
-      return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: without rotation only swiglu is routed here"); \
-    }                                                                                                   \
-    if (input_act == ACT_SWIGLU) return launch_convrot_T<TT, ACT_SWIGLU, true>(x, ldx, M, k, q, ldq, scale, st); \
-    if (input_act == ACT_GELU_TANH)                                                                     \
-      return launch_convrot_T<TT, ACT_GELU_TANH, true>(x, ldx, M, k, q, ldq, scale, st);                \
-    return launch_convrot_T<TT, ACT_NONE, true>(x, ldx, M, k, q, ldq, scale, st);                       \
-  }
-  if (x_dtype == DT_BF16) XMH3_CRA(BF16T)
-  if (x_dtype == DT_F16) XMH3_CRA(F16T)
-#undef XMH3_CRA
+  if (group_size == 0 && input_act != ACT_SWIGLU)
+    return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: without rotation only swiglu is routed here");
+  if (x_dtype == DT_BF16) return launch_convrot_act<BF16T>(x, ldx, M, k, q, ldq, scale, input_act, logg, st);
+  if (x_dtype == DT_F16) return launch_convrot_act<F16T>(x, ldx, M, k, q, ldq, scale, input_act, logg, st);
   return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: dtype must be bf16 or fp16");
 }
 
