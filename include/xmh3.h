@@ -94,6 +94,17 @@ int xmh3_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int input_act
                                        xmh3_stream_t stream);
 
 /*
+ * xmh3_quantize_int8_rowwise_convrot with the launcher's stochastic, seed
+ * pair: stochastic != 0 (seed nonzero) rounds each code as
+ * xmh3_quantize_int8_rowwise_sr does, the noise keyed by the code's index
+ * row * K + col in the [M, K] output. Replaces the same launcher
+ * (CK/backends/cuda/ops/int8_linear.cu:1295, kernel :943-1031, stochastic).
+ */
+int xmh3_quantize_int8_rowwise_convrot_sr(const void* x, int x_dtype, int input_act, int64_t M, int64_t K,
+                                          int64_t ldx, int group_size, int8_t* q, float* scale, int stochastic,
+                                          uint64_t seed, xmh3_stream_t stream);
+
+/*
  * Requantise rows whose |max| is already known (bit pattern of the fp32
  * value), the second half of the fused MLP's per-token requant.
  * Replaces the quantizer call inside the fc2 int8_linear with

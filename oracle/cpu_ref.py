@@ -236,12 +236,15 @@ def rotate_weight(w: torch.Tensor, group_size: int) -> torch.Tensor:
     return torch.matmul(w.reshape(n, k // group_size, group_size), h.T).reshape(n, k)
 
 
-def quantize_convrot(x: torch.Tensor, group_size: int = 256, input_act: str | None = None):
+def quantize_convrot(x: torch.Tensor, group_size: int = 256, input_act: str | None = None,
+                     stochastic_rounding: int | None = 0):
     """The quantizer of a rotated linear: act -> rotate -> quantize_int8_rowwise
-    (the eager order of CK/backends/eager/quantization.py:998-1023)."""
+    (the eager order of CK/backends/eager/quantization.py:998-1023); with a
+    seed, the codes are rounded stochastically with the noise of each code's
+    index in the [M, K] output (CK/backends/cuda/ops/int8_linear.cu:1019-1021)."""
     a = apply_input_act(x, input_act)
     r = rotate_activation(a, group_size)
-    q, s = quantize_int8_rowwise(r.reshape(-1, r.shape[-1]))
+    q, s = quantize_int8_rowwise(r.reshape(-1, r.shape[-1]), stochastic_rounding)
     return q, s, r
 
 

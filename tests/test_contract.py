@@ -58,8 +58,8 @@ def test_unimplemented_reference_features_raise(pkg):
         backend.int8_linear(x, torch.zeros(8, 128, dtype=torch.int8), torch.ones(8))
     with pytest.raises(ValueError, match="per-output-channel"):
         backend.int8_linear(x, w, torch.ones(3))
-    with pytest.raises(NotImplementedError, match="stochastic"):
-        backend.quantize_int8_rowwise_convrot64(x, 256, stochastic_rounding=5)
+    with pytest.raises(ValueError, match="64 bits"):
+        backend.quantize_int8_rowwise_convrot64(x, 256, stochastic_rounding=1 << 64)
     with pytest.raises(ValueError, match="64 bits"):
         backend.quantize_int8_rowwise(x, stochastic_rounding=1 << 64)
 

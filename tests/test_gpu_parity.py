@@ -873,6 +873,44 @@ def test_convrot_quantizer_group_sizes(pkg, dev, group, dtype):
     assert mism < 2e-3 and dq <= 1
 
 
+@pytest.mark.parametrize("dtype,group,act,seed", [
+    (torch.bfloat16, 256, None, 5),
+    (torch.bfloat16, 64, "swiglu", (3 << 32) + 9),
+    (torch.float16, 256, "gelu_tanh", 77),
+    (torch.float16, 1024, None, 2 ** 64 - 3),
+])
+def test_convrot_quantizer_stochastic(pkg, dev, dtype, group, act, seed):
+    """Stochastic rounding in the ConvRot quantizer on integer rows (the
+    rotation exact in any order, so the rotated row is the oracle's): codes
+    and scales bit-exact with the oracle's noise at each code's index in the
+    [M, K] output (mirrored lanes store to the right slots), and they differ
+    from the nearest codes."""
+    say(f"convrot stochastic {dtype} group {group} act={act} seed={seed}")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(group + 3)
+    m, k = 23, 2048
+    width = 2 * k if act == "swiglu" else k
+    if act == "swiglu":
+        x = torch.randint(-3, 4, (m, width), generator=g).float()   # silu(gate) * up rounds; tolerance below
+    else:
+        x = torch.randint(-30, 31, (m, width), generator=g).float()
+    x = x.to(dtype)
+    if act == "gelu_tanh":
+        x = (x.float() * 0.05).to(dtype)
+    q, s = backend.quantize_int8_rowwise_convrot64(x.to(dev), group, stochastic_rounding=seed, input_act=act)
+    q0, _ = backend.quantize_int8_rowwise_convrot64(x.to(dev), group, input_act=act)
+    torch.cuda.synchronize()
+    qr, sr, _ = cpu_ref.quantize_convrot(x, group, act, stochastic_rounding=seed)
+    if act is None:
+        assert same(q, qr, "stochastic convrot codes") and same(s, sr, "scales")
+    else:
+        assert torch.allclose(s.cpu(), sr, rtol=2 ** -7, atol=0)
+        mism, dq = _code_stats(q, qr, "stochastic convrot codes")
+        assert mism < 2e-3 and dq <= 1
+    assert not torch.equal(q.cpu(), q0.cpu())
+
+
 @pytest.mark.parametrize("act", [None, "gelu_tanh", "swiglu"])
 def test_convrot_quantizer_fp16(pkg, dev, act):
     say(f"convrot quantizer, fp16 rows, act={act}")

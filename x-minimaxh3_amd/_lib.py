@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple] = {
                                               c_void_p, c_void_p]),
     "xmh3_quantize_int8_rowwise_convrot": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_void_p,
                                                    c_void_p, c_void_p]),
+    "xmh3_quantize_int8_rowwise_convrot_sr": (c_int, [c_void_p, c_int, c_int, c_i64, c_i64, c_i64, c_int, c_void_p,
+                                                      c_void_p, c_int, ctypes.c_uint64, c_void_p]),
     "xmh3_requant_int8_rows": (c_int, [c_void_p, c_int, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_void_p]),
     "xmh3_int8_gemm": (c_int, [c_void_p, c_i64, c_void_p, c_i64, c_i64, c_i64, c_i64, c_void_p, c_void_p, c_int,
                                c_void_p, c_void_p, c_int, c_i64, c_int, c_void_p, c_void_p]),

@@ -126,6 +126,24 @@ __device__ __forceinline__ float gelu_tanh_f32(float h) {
   return h * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// Stochastic rounding noise of the reference's CUDA quantizers
+// (CK/backends/cuda/ops/int8_linear.cu:79-91): element idx (row * K + col)
+// and seed give u = (h >> 8) * 2^-24 in [0, 1), h the 32-bit PCG-RXS-M-XS
+// output hash of lo32(idx + seed) ^ hi32(idx + seed), rounded to T. A code
+// is then floor(T(v + u)) for the scaled value v.
+__device__ __forceinline__ uint32_t pcg_output_hash(uint32_t x) {
+  const uint32_t state = x * 747796405u + 2891336453u;
+  const uint32_t word = ((state >> ((state >> 28u) + 4u)) ^ state) * 277803737u;
+  return (word >> 22u) ^ word;
+}
+
+template <typename T>
+__device__ __forceinline__ float sr_noise(uint64_t idx, uint64_t seed) {
+  const uint64_t key = idx + seed;
+  const uint32_t h = pcg_output_hash((uint32_t)key ^ (uint32_t)(key >> 32));
+  return T::round((float)(h >> 8) * 0x1.0p-24f);
+}
+
 // ---------------------------------------------------------------------------
 // host-side error plumbing (no C++ exception crosses the C ABI)
 // ---------------------------------------------------------------------------

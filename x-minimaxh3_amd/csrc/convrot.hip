@@ -99,7 +99,7 @@ typedef uint32_t cr_u32x4 __attribute__((ext_vector_type(4)));
 template <typename T, int ACT, int LOGG, int NIT>
 __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
     const typename T::storage* __restrict__ x, int64_t ldx, int K, int8_t* __restrict__ q, int64_t ldq,
-    float* __restrict__ scale) {
+    float* __restrict__ scale, uint64_t seed) {
   using S = typename T::storage;
   __shared__ float wave_amax[8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = blockDim.x >> 6;
@@ -192,10 +192,18 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
   const float inv = 1.0f / sT;
   const float inv_v = inv * unfold;       // applied to the kept values
   int8_t* qr = q + row * ldq;
+  constexpr int mirror = (LOGG >= 3 ? 3 : 0) | (LOGG >= 4 ? 12 : 0);
+  const int slot = g16 ^ mirror;
+  // stochastic rounding (seed != 0): code = floor(T(v + noise)) with the
+  // noise of element row * K + col of the [M, K] codes, v the value the
+  // nearest path rounds
+  const bool sr = seed != 0;
+  const uint64_t rbase = (uint64_t)row * (uint64_t)K;
 #pragma unroll
   for (int it = 0; it < NIT; ++it) {
     const int group = (it * nwaves + wave) * 4 + (lane >> 4);
     if (group >= groups) continue;
+    const uint64_t cbase = rbase + (uint64_t)(group * 256 + slot * 16);
     uint32_t w[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -205,7 +213,8 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
         uint32_t y[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const float c = T::round(T::round(keepf[it][4 * k + b]) * inv_v);
+          float c = T::round(T::round(keepf[it][4 * k + b]) * inv_v);
+          if (sr) c = floorf(T::round(c + sr_noise<T>(cbase + 4 * k + b, seed)));
           y[b] = __float_as_uint(__builtin_amdgcn_fmed3f(c, -128.0f, 127.0f) + 12582912.0f);
         }
         const uint32_t lo = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u);
@@ -217,15 +226,14 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
         for (int b = 0; b < 4; ++b) {
           const int i = 4 * k + b;
           const float r = T::load((keep[it][i >> 1] >> (16 * (i & 1))) & 0xffffu);
-          float code = rintf(T::round(r / sT));
+          const float v = T::round(r / sT);
+          float code = sr ? floorf(T::round(v + sr_noise<T>(cbase + i, seed))) : rintf(v);
           code = fminf(fmaxf(code, -128.0f), 127.0f);
           word |= (uint32_t)((int)code & 0xff) << (8 * b);
         }
         w[k] = word;
       }
     }
-    constexpr int mirror = (LOGG >= 3 ? 3 : 0) | (LOGG >= 4 ? 12 : 0);
-    const int slot = g16 ^ mirror;
     *reinterpret_cast<uint4*>(qr + group * 256 + slot * 16) = make_uint4(w[0], w[1], w[2], w[3]);
   }
   if (threadIdx.x == 0) scale[row] = s;
@@ -233,7 +241,7 @@ __global__ __launch_bounds__(512) void convrot_quant_rows_kernel(
 
 template <typename T, int ACT, int LOGG>
 static int launch_convrot_T(const void* x, int64_t ldx, int64_t M, int K, int8_t* q, int64_t ldq, float* scale,
-                            hipStream_t st) {
+                            uint64_t seed, hipStream_t st) {
   using S = typename T::storage;
   // wave-iterations of four groups each; at most 16 (K <= 16384)
   const int quads = (K / 256 + 3) / 4;
@@ -243,37 +251,39 @@ static int launch_convrot_T(const void* x, int64_t ldx, int64_t M, int K, int8_t
   const dim3 grid((unsigned)M), block((unsigned)(64 * waves));
   if (nit == 1)
     hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, LOGG, 1>), grid, block, 0, st, static_cast<const S*>(x),
-                       ldx, K, q, ldq, scale);
+                       ldx, K, q, ldq, scale, seed);
   else
     hipLaunchKernelGGL((convrot_quant_rows_kernel<T, ACT, LOGG, 2>), grid, block, 0, st, static_cast<const S*>(x),
-                       ldx, K, q, ldq, scale);
+                       ldx, K, q, ldq, scale, seed);
   return check_launch("convrot_quant_rows_kernel");
 }
 
 template <typename T, int ACT>
 static int launch_convrot_g(const void* x, int64_t ldx, int64_t M, int K, int8_t* q, int64_t ldq, float* scale,
-                            int logg, hipStream_t st) {
+                            int logg, uint64_t seed, hipStream_t st) {
   switch (logg) {
-    case 1: return launch_convrot_T<T, ACT, 1>(x, ldx, M, K, q, ldq, scale, st);
-    case 2: return launch_convrot_T<T, ACT, 2>(x, ldx, M, K, q, ldq, scale, st);
-    case 3: return launch_convrot_T<T, ACT, 3>(x, ldx, M, K, q, ldq, scale, st);
-    case 4: return launch_convrot_T<T, ACT, 4>(x, ldx, M, K, q, ldq, scale, st);
-    case 5: return launch_convrot_T<T, ACT, 5>(x, ldx, M, K, q, ldq, scale, st);
+    case 1: return launch_convrot_T<T, ACT, 1>(x, ldx, M, K, q, ldq, scale, seed, st);
+    case 2: return launch_convrot_T<T, ACT, 2>(x, ldx, M, K, q, ldq, scale, seed, st);
+    case 3: return launch_convrot_T<T, ACT, 3>(x, ldx, M, K, q, ldq, scale, seed, st);
+    case 4: return launch_convrot_T<T, ACT, 4>(x, ldx, M, K, q, ldq, scale, seed, st);
+    case 5: return launch_convrot_T<T, ACT, 5>(x, ldx, M, K, q, ldq, scale, seed, st);
     default: return fail(XMH3_EINVAL, "quantize_int8_rowwise_convrot: bad group size");
   }
 }
 
 template <typename T>
 static int launch_convrot_act(const void* x, int64_t ldx, int64_t M, int K, int8_t* q, int64_t ldq, float* scale,
-                              int input_act, int logg, hipStream_t st) {
-  if (logg == 0) return launch_convrot_T<T, ACT_SWIGLU, 0>(x, ldx, M, K, q, ldq, scale, st);
-  if (input_act == ACT_SWIGLU) return launch_convrot_g<T, ACT_SWIGLU>(x, ldx, M, K, q, ldq, scale, logg, st);
-  if (input_act == ACT_GELU_TANH) return launch_convrot_g<T, ACT_GELU_TANH>(x, ldx, M, K, q, ldq, scale, logg, st);
-  return launch_convrot_g<T, ACT_NONE>(x, ldx, M, K, q, ldq, scale, logg, st);
+                              int input_act, int logg, uint64_t seed, hipStream_t st) {
+  if (logg == 0) return launch_convrot_T<T, ACT_SWIGLU, 0>(x, ldx, M, K, q, ldq, scale, seed, st);
+  if (input_act == ACT_SWIGLU)
+    return launch_convrot_g<T, ACT_SWIGLU>(x, ldx, M, K, q, ldq, scale, logg, seed, st);
+  if (input_act == ACT_GELU_TANH)
+    return launch_convrot_g<T, ACT_GELU_TANH>(x, ldx, M, K, q, ldq, scale, logg, seed, st);
+  return launch_convrot_g<T, ACT_NONE>(x, ldx, M, K, q, ldq, scale, logg, seed, st);
 }
 
 int quantize_rows_convrot(const void* x, int x_dtype, int input_act, int64_t M, int64_t K, int64_t ldx,
-                          int group_size, int8_t* q, int64_t ldq, float* scale, hipStream_t st) {
+                          int group_size, int8_t* q, int64_t ldq, float* scale, uint64_t seed, hipStream_t st) {
   XMH3_REQUIRE(M >= 0 && K >= 0, "quantize_int8_rowwise_convrot: negative size");
   int logg = 0;
   while (logg < 6 && (1 << (2 * logg)) < group_size) ++logg;
@@ -293,8 +303,8 @@ int quantize_rows_convrot(const void* x, int x_dtype, int input_act, int64_t M, 
   const int k = (int)K;
   if (group_size == 0 && input_act != ACT_SWIGLU)
     return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: without rotation only swiglu is routed here");
-  if (x_dtype == DT_BF16) return launch_convrot_act<BF16T>(x, ldx, M, k, q, ldq, scale, input_act, logg, st);
-  if (x_dtype == DT_F16) return launch_convrot_act<F16T>(x, ldx, M, k, q, ldq, scale, input_act, logg, st);
+  if (x_dtype == DT_BF16) return launch_convrot_act<BF16T>(x, ldx, M, k, q, ldq, scale, input_act, logg, seed, st);
+  if (x_dtype == DT_F16) return launch_convrot_act<F16T>(x, ldx, M, k, q, ldq, scale, input_act, logg, seed, st);
   return fail(XMH3_EUNSUPPORTED, "quantize_int8_rowwise_convrot: dtype must be bf16 or fp16");
 }
 
@@ -303,5 +313,15 @@ int quantize_rows_convrot(const void* x, int x_dtype, int input_act, int64_t M, 
 extern "C" int xmh3_quantize_int8_rowwise_convrot(const void* x, int x_dtype, int input_act, int64_t M,
                                                   int64_t K, int64_t ldx, int group_size, int8_t* q,
                                                   float* scale, hipStream_t stream) {
-  return xmh3::quantize_rows_convrot(x, x_dtype, input_act, M, K, ldx, group_size, q, K, scale, stream);
+  return xmh3::quantize_rows_convrot(x, x_dtype, input_act, M, K, ldx, group_size, q, K, scale, 0, stream);
+}
+
+extern "C" int xmh3_quantize_int8_rowwise_convrot_sr(const void* x, int x_dtype, int input_act, int64_t M,
+                                                     int64_t K, int64_t ldx, int group_size, int8_t* q,
+                                                     float* scale, int stochastic, uint64_t seed,
+                                                     hipStream_t stream) {
+  if (stochastic && seed == 0)
+    return xmh3::fail(xmh3::XMH3_EINVAL, "quantize_int8_rowwise_convrot: a stochastic seed must be nonzero");
+  return xmh3::quantize_rows_convrot(x, x_dtype, input_act, M, K, ldx, group_size, q, K, scale,
+                                     stochastic ? seed : 0, stream);
 }

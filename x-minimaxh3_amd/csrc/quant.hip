@@ -347,22 +347,9 @@ __global__ __launch_bounds__(256) void requant_rows_kernel(
 // rounding of the exact sum: when the exact sum of two T values does not fit
 // fp32's 24 bits, the smaller one lies below 2^-15 (bf16; 2^-12 for fp16) of
 // the larger and cannot reach T's half-step, while every T tie is an exact
-// fp32 sum. One block per row; the second pass re-reads the row (mostly
-// from L2).
+// fp32 sum (pcg_output_hash / sr_noise in common.hpp). One block per row;
+// the second pass re-reads the row (mostly from L2).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t pcg_output_hash(uint32_t x) {
-  const uint32_t state = x * 747796405u + 2891336453u;
-  const uint32_t word = ((state >> ((state >> 28u) + 4u)) ^ state) * 277803737u;
-  return (word >> 22u) ^ word;
-}
-
-template <typename T>
-__device__ __forceinline__ float sr_noise(uint64_t idx, uint64_t seed) {
-  const uint64_t key = idx + seed;
-  const uint32_t h = pcg_output_hash((uint32_t)key ^ (uint32_t)(key >> 32));
-  return T::round((float)(h >> 8) * 0x1.0p-24f);
-}
-
 template <typename T>
 __global__ __launch_bounds__(256) void quant_rows_sr_kernel(
     const typename T::storage* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
