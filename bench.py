@@ -491,7 +491,7 @@ def main() -> int:
                          "achieved": round(fc2_tops, 2), "peak": PEAK_INT8_TOPS, "unit": "TFLOP/s",
                          "frac": round(fc2_tops / PEAK_INT8_TOPS, 4),
                          "traffic": round(TRAFFIC_BYTES["fc2_gemm"])},
-        "norm_rope": {"kernel": "norm_rope_pipe_kernel (Q and K)", "bound": "hbm", "achieved": round(nr_gbs, 1),
+        "norm_rope": {"kernel": "norm_rope_coop_kernel (Q and K)", "bound": "hbm", "achieved": round(nr_gbs, 1),
                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(nr_gbs / PEAK_HBM_GBS, 4),
                       "us_per_launch": round(nr_ms * 1e3, 2), "traffic": round(TRAFFIC_BYTES["norm_rope"]),
                       "algorithmic": "8*M*d bytes (Q,K read + written, bf16)"},

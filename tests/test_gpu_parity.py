@@ -501,21 +501,25 @@ def test_norm_rope_720p(pkg, dev):
         assert same(got, want, f"norm_rope {name}")   # reference reduction order -> bit exact
 
 
-@pytest.mark.parametrize("d,m,with_k,tab_dtype,bcast", [
-    (5120, 37, True, torch.float32, False),     # pipelined kernel, fewer rows than waves
-    (5120, 1000, False, torch.float32, False),  # Q only
-    (3072, 1000, True, torch.bfloat16, False),  # bf16 table
-    (1024, 4099, True, torch.float32, True),    # one broadcast table row
-    (4096, 1, True, torch.float32, False),      # a single token
-    (1536, 300, True, torch.float32, False),    # width not a multiple of 1024 -> row kernel
+@pytest.mark.parametrize("d,m,with_k,tab_dtype,bcast,dtype", [
+    (5120, 37, True, torch.float32, False, torch.bfloat16),    # cooperative kernel, fewer tokens than blocks
+    (5120, 1000, False, torch.float32, False, torch.bfloat16),  # Q only
+    (3072, 1000, True, torch.bfloat16, False, torch.bfloat16),  # bf16 table
+    (1024, 4099, True, torch.float32, True, torch.bfloat16),    # one broadcast table row
+    (4096, 1, True, torch.float32, False, torch.bfloat16),      # a single token
+    (8192, 333, True, torch.float32, False, torch.bfloat16),    # 16 waves per block
+    (8192, 120, False, torch.float32, False, torch.bfloat16),   # Q only, 8 waves per row
+    (2048, 700, True, torch.float16, False, torch.float16),     # fp16 rows and table
+    (5120, 257, True, torch.float32, False, torch.float16),     # fp16 rows, fp32 table
+    (1536, 300, True, torch.float32, False, torch.bfloat16),    # width not a multiple of 1024 -> row kernel
 ])
-def test_norm_rope_shapes(pkg, dev, d, m, with_k, tab_dtype, bcast):
-    say(f"norm_rope d={d} m={m} k={with_k} table={tab_dtype} broadcast={bcast}")
+def test_norm_rope_shapes(pkg, dev, d, m, with_k, tab_dtype, bcast, dtype):
+    say(f"norm_rope d={d} m={m} k={with_k} table={tab_dtype} broadcast={bcast} x={dtype}")
     g = torch.Generator().manual_seed(d + m)
-    q = torch.randn(m, d, generator=g).to(torch.bfloat16)
-    k = torch.randn(m, d, generator=g).to(torch.bfloat16)
-    scale = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
-    shift = (torch.randn(1, d, generator=g) * 0.1).to(torch.bfloat16)
+    q = torch.randn(m, d, generator=g).to(dtype)
+    k = torch.randn(m, d, generator=g).to(dtype)
+    scale = (torch.randn(1, d, generator=g) * 0.1).to(dtype)
+    shift = (torch.randn(1, d, generator=g) * 0.1).to(dtype)
     ang = torch.rand(1, 1 if bcast else m, 1, 64, generator=g) * 40
     c, s = torch.cos(ang), torch.sin(ang)
     tab = torch.stack((c, -s, s, c), -1).reshape(1, ang.shape[1], 1, 64, 2, 2).to(tab_dtype)

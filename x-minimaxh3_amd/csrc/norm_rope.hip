@@ -415,26 +415,6 @@ __global__ __launch_bounds__(256) void rowspan_exact_kernel(RowArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined norm-rope (single modulation row per launch).
-//
-// Persistent waves: wave w of the grid handles rows w, w + W, w + 2W, ... of
-// the (token, tensor) row list (row r = token * nt + tensor, nt = 1 or 2 for Q
-// only or Q and K), two rows ahead: while row i is reduced, normalised,
-// rotated and stored, the 16-byte loads of rows i+1 and i+2 are in flight in
-// two register buffers. A row's bytes land in the wave's LDS slice (row +
-// its RoPE table row) before the reduction, which runs in the reference's
-// order (ref_order_sumsq); the element pass then reads the row back from LDS.
-// The modulation (1 + scale rounded to the scale dtype, and shift) is the same
-// for every row, so the block turns it into fp32 once, in LDS, at start.
-// Nothing but the row and table loads goes through the vector-memory counter,
-// so waiting for row i never waits for anything issued later.
-//
-// LDS: WPB * (D * sizeof(x) + table row) + 2 * D * 4 bytes.
-// Items: u = s * 64 + lane (s < NSTEP), the 8 elements at head offset
-// 8 * (u % 8) and the 8 at +64 (head_dim 128, 8 items per head). Every lane
-// holds NSTEP items (D == 1024 * NSTEP): no predicated memory operation, so
-// the compiler's wait counts track both prefetched rows exactly.
-// ---------------------------------------------------------------------------
 // LDS placement of a staged row: element p of head h = p / 128 sits in half
 // ((p / 64) & 1) ^ flip(h) of the head's 256 bytes. flip alternates between
 // the heads one 64-lane access touches (8 consecutive heads for the 16-byte
@@ -448,31 +428,66 @@ struct SwizzledRowIdx {
   }
 };
 
-template <typename TX, typename TF, bool ADALN, int NSTEP>
-__global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) {
+// ---------------------------------------------------------------------------
+// Cooperative norm-rope: a row is split over P = D / 1024 waves; wave p of a
+// row owns the 1024 consecutive elements (8 heads) [1024 p, 1024 p + 1024).
+// A block of R * P waves takes the R consecutive rows of a row group per
+// iteration; the rows are ordered all Q rows, then all K rows (row r: tensor
+// r / tokens), and the blocks (one per CU) visit groups blockIdx.x,
+// + gridDim.x, ..., so the accesses in flight at any time cover one dense
+// window of one tensor. A plain copy of the same bytes measured 168 us in
+// this form; a wave per whole row (the waves' accesses spread over as many
+// rows as waves) took 190 us, a block per token with its Q and K rows
+// 179 us, and more blocks per CU were slower. R rows per block keep R rows'
+// reductions and element passes in flight at once (one row per block left
+// the CU latency-bound: 278 us).
+//
+// The reference-order sum of squares (ref_order_sumsq) is a fold over chunks
+// of 512 positions: chain L adds the 16 squares at 512 j + 32 u + L from zero
+// (u = 0..15) and folds the chunk sum into its cascade. A part holds chunks
+// 2 p and 2 p + 1 whole, so each wave computes its 2 x 32 chunk sums from its
+// staged part, the block shares them in LDS, and after one barrier every
+// wave folds the row's 2P chunk sums in order and combines the chains as
+// ref_order_sumsq does: bit-identical rrms. D % 1024 == 0 leaves no partial
+// chunk and no leftover vector.
+//
+// Two rows are prefetched in registers (2 items of 16 bytes per lane per row,
+// plus the row's table row, 16 bytes per lane). Chunk sums and the table row
+// live in two parity slots, so one barrier per row suffices: a slot is
+// rewritten two rows later, after every wave has passed the barrier that
+// follows its last read. The barrier waits for LDS only (__syncthreads would
+// also wait for the prefetched loads).
+// LDS: 8 D (modulation, ADALN) + 2 KB per wave (staging) + 2 * R * 2P * 32
+// floats (chunk sums) + 2 R table rows.
+// ---------------------------------------------------------------------------
+template <typename TX, typename TF, bool ADALN, int P>
+__global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt) {
   using S = typename TX::storage;
   using SF = typename TF::storage;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   typedef float f32x4 __attribute__((ext_vector_type(4)));
-  constexpr int HD = 128, IPH = HD / 16, TAB_ELEMS = HD / 2 * 4;
-  constexpr int TAB_CHUNKS = TAB_ELEMS * (int)sizeof(SF) / 16;   // 16-byte pieces of a table row
-  constexpr int EPC = 16 / (int)sizeof(SF);                      // table elements per piece
-  constexpr int CPG = TAB_CHUNKS / IPH;                          // pieces per 8-pair group
-  constexpr int D = NSTEP * 1024;
+  static_assert(sizeof(S) == 2, "16-bit rows");
+  constexpr int HD = 128, IPH = HD / 16, D = P * 1024, NCH = 2 * P;
+  constexpr int TAB_BYTES = (HD / 2) * 4 * (int)sizeof(SF);
+  constexpr int TAB_CHUNKS = TAB_BYTES / 16;
+  constexpr int CPG = TAB_CHUNKS / IPH;                          // 16-byte pieces per 8-pair group
+  constexpr int EPC = 16 / (int)sizeof(SF);
   extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wpb = blockDim.x >> 6;
-  // modulation, lane-major: float4 (((s * 2 + half) * 2 + quad) * 64 + lane)
-  // holds columns col(s, half, lane) + 4 * quad .. + 3
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int R = (blockDim.x >> 6) / P;                                 // rows per block iteration
+  const int sub = w / P, part = w - sub * P;
   f32x4* lt = reinterpret_cast<f32x4*>(dyn_lds);
   f32x4* ls = lt + D / 4;
-  uint8_t* wbase = dyn_lds + (ADALN ? 8 * D : 0) + wave * (D * (int)sizeof(S) + TAB_ELEMS * (int)sizeof(SF));
-  S* lrow = reinterpret_cast<S*>(wbase);
-  u32x4* ltab = reinterpret_cast<u32x4*>(wbase + D * (int)sizeof(S));
+  uint8_t* p0 = dyn_lds + (ADALN ? 8 * D : 0);
+  S* stage = reinterpret_cast<S*>(p0 + w * 2048);
+  float* sums = reinterpret_cast<float*>(p0 + R * P * 2048);           // [2][R][NCH][32]
+  u32x4* tabs = reinterpret_cast<u32x4*>(sums + 2 * R * NCH * 32);     // [2][R][TAB_CHUNKS]
 
   if constexpr (ADALN) {
-    // t = round_TX(1 + scale), sh = shift, as fp32 (one modulation row)
+    // t = round_TX(1 + scale), sh = shift, as fp32, lane-major: float4
+    // (((part * 2 + half) * 2 + quad) * 64 + lane) holds the columns of item
+    // half of that lane in that part, + 4 * quad .. + 3
     const S* sc = static_cast<const S*>(a.scale);
     const S* sh = static_cast<const S*>(a.shift);
     for (int i = threadIdx.x; i < D / 4; i += blockDim.x) {
@@ -488,70 +503,98 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
       lt[i] = tv;
       ls[i] = sv;
     }
-    __syncthreads();
   }
+  __syncthreads();
 
-  const int nrows = (int)a.rows * nt;
-  const int stride = gridDim.x * wpb;
-  const int tshift = nt - 1;            // token = row >> tshift, tensor = row & tshift
-  int r = blockIdx.x * wpb + wave;
-  if (r >= nrows) return;
+  const int64_t ntok = a.rows, nrows = ntok * nt, ngroups = (nrows + R - 1) / R;
+  const int64_t G = gridDim.x;
+  int64_t g = blockIdx.x;
+  if (g >= ngroups) return;   // uniform per block
 
-  // Item slots of this lane (the same for every row). Step s adds 8 heads
-  // (1024 elements) and leaves row_flip unchanged (it depends on the head's
-  // bits 0 and 2 only), so every slot is a per-lane base plus a constant.
   const int qh = lane / IPH, it8 = (lane % IPH) * 8;
-  const int obase = qh * HD + it8;
-  const int sbase0 = qh * HD + (row_flip(qh) << 6) + it8;
-  const int sbase1 = qh * HD + ((row_flip(qh) ^ 1) << 6) + it8;
-  auto off0 = [&](int s) { return obase + s * 1024; };
-  auto off1 = [&](int s) { return obase + s * 1024 + HD / 2; };
-  auto slot0 = [&](int s) { return sbase0 + s * 1024; };
-  auto slot1 = [&](int s) { return sbase1 + s * 1024; };
+  const int o0 = part * 1024 + qh * HD + it8;                         // item 0; item 1 at + 64
+  const int sl0 = qh * HD + (row_flip(qh) << 6) + it8;                 // staged (SwizzledRowIdx)
+  const int sl1 = qh * HD + ((row_flip(qh) ^ 1) << 6) + it8;
   const int tab_lane = min(lane, TAB_CHUNKS - 1);
   // table piece c = tab_lane goes to slot (c % CPG) * 8 + c / CPG, so the
   // lanes of one 8-pair group read consecutive slots
   const int tab_slot = (tab_lane % CPG) * IPH + tab_lane / CPG;
 
-  // loads of one row into a buffer; past the last row the last row is
-  // re-read (never processed), so every wave issues the same sequence
-  auto issue = [&](int row, u32x4 (&bx)[NSTEP][2], u32x4& bt) __attribute__((always_inline)) {
+  // this wave's row in group gg; past the end, the last row is read again
+  // (computed, never stored) so every wave keeps the block's barriers
+  auto issue = [&](int64_t gg, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
+    int64_t row = gg * R + sub;
     row = row < nrows ? row : nrows - 1;
-    const int64_t tok = row >> tshift;
-    const S* xb = static_cast<const S*>((row & tshift) ? a.x1 : a.x0) + tok * a.ldx;
-#pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {   // streamed once: non-temporal
-      bx[s][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + off0(s)));
-      bx[s][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + off1(s)));
-    }
+    const int64_t tok = row < ntok ? row : row - ntok;
+    const S* xb = static_cast<const S*>(row < ntok ? a.x0 : a.x1) + tok * a.ldx + o0;
+    bx[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb));
+    bx[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + HD / 2));
     const SF* tb = static_cast<const SF*>(a.freqs) + (a.freqs_row_stride ? tok * a.freqs_row_stride : 0);
     bt = *reinterpret_cast<const u32x4*>(tb + tab_lane * EPC);
   };
 
-  auto process = [&](int row, u32x4 (&bx)[NSTEP][2], u32x4& bt) __attribute__((always_inline)) {
-    // stage row + table in LDS
-#pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-      *reinterpret_cast<u32x4*>(lrow + slot0(s)) = bx[s][0];
-      *reinterpret_cast<u32x4*>(lrow + slot1(s)) = bx[s][1];
-    }
-    if (lane < TAB_CHUNKS) ltab[tab_slot] = bt;
-    // the buffer is free again: loads of row i+2, kept in program order
-    // (ahead of this row's stores) so the next wait can leave them in flight
+  int par = 0;
+  auto process = [&](int64_t gg, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
+    const int64_t row = gg * R + sub;
+    const int slot = par * R + sub;
+    *reinterpret_cast<u32x4*>(stage + sl0) = bx[0];
+    *reinterpret_cast<u32x4*>(stage + sl1) = bx[1];
+    if (part == 0 && lane < TAB_CHUNKS) tabs[slot * TAB_CHUNKS + tab_slot] = bt;
     __builtin_amdgcn_sched_barrier(0);
-    issue(row + 2 * stride, bx, bt);
+    issue(gg + 2 * G, bx, bt);
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS stores done
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's staging stores done
     __builtin_amdgcn_wave_barrier();
-    const float tot = ref_order_sumsq<TX>(lrow, D, lane, SwizzledRowIdx{});
-    const float rr = 1.0f / sqrtf(tot / (float)D + a.eps);
-    // this lane's 8 pairs (it * 8 .. it * 8 + 7) of the table row
+    {
+      // chunk 2 part + h of chain L: 16 squares in order, from zero
+      const int L = lane & 31, h = lane >> 5;
+      float c = 0.0f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const float v = TX::load(stage[SwizzledRowIdx{}(h * 512 + u * 32 + L)]);
+        c = add_sq<TX>(c, v);
+      }
+      sums[(slot * NCH + 2 * part + h) * 32 + L] = c;
+    }
+    // publish the chunk sums (and wave 0's table row) to the block
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_barrier" ::: "memory");
+    float rr;
+    {
+      // the reference order: fold the row's chunk sums, then the chains
+      const int L = lane & 31;
+      const float* cs = sums + slot * NCH * 32 + L;
+      float acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        acc1 = acc1 + cs[j * 32];
+        const int i_end = (j + 1) * 16;
+        if ((i_end & (15 << 4)) == 0) {
+          acc2 = acc2 + acc1;
+          acc1 = 0.0f;
+          if ((i_end & (15 << 8)) == 0) {
+            acc3 = acc3 + acc2;
+            acc2 = 0.0f;
+          }
+        }
+      }
+      const float tot = ((0.0f + acc1) + acc2) + acc3;
+      const int v8 = lane & 7;
+      const float r0 = __shfl(tot, v8, 64), r1 = __shfl(tot, v8 + 8, 64);
+      const float r2 = __shfl(tot, v8 + 16, 64), r3 = __shfl(tot, v8 + 24, 64);
+      const float pv = ((r0 + r1) + r2) + r3;
+      float fin = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) fin = fin + __shfl(pv, v, 64);
+      rr = 1.0f / sqrtf(fin / (float)D + a.eps);
+    }
+    // this lane's 8 pairs (it8 .. it8 + 7) of the token's table row
     Tab8<TF> tab;
     {
       SF el[CPG * EPC];
 #pragma unroll
       for (int j = 0; j < CPG; ++j) {
-        const u32x4 v = ltab[j * IPH + (lane % IPH)];
+        const u32x4 v = tabs[slot * TAB_CHUNKS + j * IPH + (lane % IPH)];
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
           if constexpr (sizeof(SF) == 4) el[j * EPC + e] = __uint_as_float(v[e]);
@@ -563,77 +606,76 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
 #pragma unroll
         for (int e = 0; e < 4; ++e) tab.f[pp][e] = TF::load(el[pp * 4 + e]);
     }
-    const int64_t tok = row >> tshift;
-    S* ob = static_cast<S*>((row & tshift) ? a.o1 : a.o0) + tok * a.ldo;
+    float y[2][8];
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
-      float y[2][8];
+    for (int h = 0; h < 2; ++h) {
+      V8<TX> xv;
+      xv.v = *reinterpret_cast<const uint4*>(stage + (h ? sl1 : sl0));
+      float t8[8], sh8[8];
+      if constexpr (ADALN) {
+        const int i0 = ((part * 2 + h) * 2) * 64 + lane;
+        const f32x4 ta = lt[i0], tb2 = lt[i0 + 64], sa = ls[i0], sb = ls[i0 + 64];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        V8<TX> xv;
-        xv.v = *reinterpret_cast<const uint4*>(lrow + (h ? slot1(s) : slot0(s)));
-        float t8[8], sh8[8];
-        if constexpr (ADALN) {
-          const int i0 = ((s * 2 + h) * 2) * 64 + lane;
-          const f32x4 ta = lt[i0], tb2 = lt[i0 + 64], sa = ls[i0], sb = ls[i0 + 64];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            t8[e] = ta[e]; t8[e + 4] = tb2[e];
-            sh8[e] = sa[e]; sh8[e + 4] = sb[e];
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j += 2) {
-          float n0 = g8<TX>(xv, j) * rr, n1 = g8<TX>(xv, j + 1) * rr;
-          TX::round2(n0, n1);                      // rms_norm output in x's dtype
-          if constexpr (ADALN) {
-            n0 = n0 * t8[j]; n1 = n1 * t8[j + 1];
-            TX::round2(n0, n1);
-            n0 = n0 + sh8[j]; n1 = n1 + sh8[j + 1];
-            TX::round2(n0, n1);
-          }
-          y[h][j] = n0;
-          y[h][j + 1] = n1;
+        for (int e = 0; e < 4; ++e) {
+          t8[e] = ta[e]; t8[e + 4] = tb2[e];
+          sh8[e] = sa[e]; sh8[e + 4] = sb[e];
         }
       }
-      uint32_t w0[4], w1[4];
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
-        float p0[2], p1[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float a0 = TF::round(y[0][j + e]), a1 = TF::round(y[1][j + e]);
-          const float* f = tab.f[j + e];
-          p0[e] = TF::round(TF::round(f[0] * a0) + TF::round(f[1] * a1));
-          p1[e] = TF::round(TF::round(f[2] * a0) + TF::round(f[3] * a1));
+        float n0 = g8<TX>(xv, j) * rr, n1 = g8<TX>(xv, j + 1) * rr;
+        TX::round2(n0, n1);                      // rms_norm output in x's dtype
+        if constexpr (ADALN) {
+          n0 = n0 * t8[j]; n1 = n1 * t8[j + 1];
+          TX::round2(n0, n1);
+          n0 = n0 + sh8[j]; n1 = n1 + sh8[j + 1];
+          TX::round2(n0, n1);
         }
-        w0[j >> 1] = TX::store2(p0[0], p0[1]);
-        w1[j >> 1] = TX::store2(p1[0], p1[1]);
+        y[h][j] = n0;
+        y[h][j + 1] = n1;
       }
-      __builtin_nontemporal_store(u32x4{w0[0], w0[1], w0[2], w0[3]}, reinterpret_cast<u32x4*>(ob + off0(s)));
-      __builtin_nontemporal_store(u32x4{w1[0], w1[1], w1[2], w1[3]}, reinterpret_cast<u32x4*>(ob + off1(s)));
     }
-    // the next row's staging overwrites this wave's LDS slice: every lane's
-    // reads of it must be done
+    uint32_t w0[4], w1[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      float q0[2], q1[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float a0 = TF::round(y[0][j + e]), a1 = TF::round(y[1][j + e]);
+        const float* f = tab.f[j + e];
+        q0[e] = TF::round(TF::round(f[0] * a0) + TF::round(f[1] * a1));
+        q1[e] = TF::round(TF::round(f[2] * a0) + TF::round(f[3] * a1));
+      }
+      w0[j >> 1] = TX::store2(q0[0], q0[1]);
+      w1[j >> 1] = TX::store2(q1[0], q1[1]);
+    }
+    if (row < nrows) {
+      const int64_t tok = row < ntok ? row : row - ntok;
+      S* ob = static_cast<S*>(row < ntok ? a.o0 : a.o1) + tok * a.ldo + o0;
+      __builtin_nontemporal_store(u32x4{w0[0], w0[1], w0[2], w0[3]}, reinterpret_cast<u32x4*>(ob));
+      __builtin_nontemporal_store(u32x4{w1[0], w1[1], w1[2], w1[3]}, reinterpret_cast<u32x4*>(ob + HD / 2));
+    }
+    // the next row's staging overwrites this wave's slice
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    par ^= 1;
   };
 
-  // The first row is peeled off the loop so that the loop is entered with the
-  // same memory operations outstanding as it has on its back edge; the
-  // compiler's wait counts then leave the second prefetched row in flight.
-  u32x4 x0[NSTEP][2], x1[NSTEP][2], t0, t1;
-  issue(r, x0, t0);
-  issue(r + stride, x1, t1);
+  // the first group is peeled off the loop so that the loop is entered with
+  // the same loads outstanding as on its back edge: the compiler's wait
+  // counts then leave the second prefetched group in flight
+  u32x4 x0[2], x1[2], t0, t1;
+  issue(g, x0, t0);
+  issue(g + G, x1, t1);
   __builtin_amdgcn_sched_barrier(0);
-  process(r, x0, t0);
-  r += stride;
-  while (r < nrows) {
-    process(r, x1, t1);
-    r += stride;
-    if (r >= nrows) break;
-    process(r, x0, t0);
-    r += stride;
+  process(g, x0, t0);
+  g += G;
+  while (g < ngroups) {
+    process(g, x1, t1);
+    g += G;
+    if (g >= ngroups) break;
+    process(g, x0, t0);
+    g += G;
   }
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): no load lands after the wave ends
 }
@@ -643,8 +685,9 @@ __global__ __launch_bounds__(512) void norm_rope_pipe_kernel(RowArgs a, int nt) 
 // modulation has the rows' dtype.
 //
 // Block b owns the contiguous rows [b * chunk, (b + 1) * chunk); its waves take
-// rows first + wave, first + wave + WPB, ..., two rows ahead, as in the
-// norm-rope pipe kernel above. The block caches in LDS round(1 + scale), shift
+// rows first + wave, first + wave + WPB, ..., two rows ahead (loads of rows
+// i + 1 and i + 2 in flight in two register buffers while row i is
+// reduced, modulated and stored). The block caches in LDS round(1 + scale), shift
 // and the norm weight of its first row's modulation row; a row with another
 // modulation row (a block that straddles a segment or sample boundary) reads
 // its modulation from global memory, which costs that row the prefetch
@@ -776,8 +819,8 @@ __global__ __launch_bounds__(512) void adaln_pipe_kernel(RowArgs a, int64_t chun
     __builtin_amdgcn_wave_barrier();
   };
 
-  // first row peeled off the loop, as in the norm-rope pipe kernel, so that
-  // the loop is entered with the memory operations of its back edge in flight
+  // first row peeled off the loop so that the loop is entered with the
+  // memory operations of its back edge in flight
   u32x4 x0[NSTEP], x1[NSTEP];
   issue(r, x0);
   issue(r + stride, x1);
@@ -1111,34 +1154,6 @@ static int cu_count() {
 
 constexpr size_t LDS_BYTES = 160 * 1024;   // gfx950 LDS per workgroup
 
-// Persistent launch of the pipelined norm-rope kernel. Returns -1 (no launch)
-// when the row does not fit the kernel's LDS plan.
-template <typename TX, typename TF, bool ADALN, int N>
-static int launch_pipe_n(RowArgs& a, int nt, hipStream_t st) {
-  const size_t per_wave = (size_t)a.D * sizeof(typename TX::storage) + 64 * 4 * sizeof(typename TF::storage);
-  const size_t mod = ADALN ? 8 * (size_t)a.D : 0;
-  if (mod + per_wave > LDS_BYTES) return -1;
-  const int wpb = (int)std::min<size_t>(8, (LDS_BYTES - mod) / per_wave);
-  const size_t lds = mod + (size_t)wpb * per_wave;
-  auto kern = norm_rope_pipe_kernel<TX, TF, ADALN, N>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES) !=
-        hipSuccess)
-      return fail(XMH3_EHIP, "norm-rope kernel: cannot raise the dynamic LDS limit");
-    attr_set = true;
-  }
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * wpb, lds) != hipSuccess || per_cu < 1)
-    per_cu = 1;
-  const int cus = std::max(1, cu_count());
-  const int64_t nrows = a.rows * nt;
-  const int64_t grid = std::min<int64_t>((nrows + wpb - 1) / wpb, (int64_t)cus * per_cu);
-  if (nrows + 2 * grid * wpb >= (1LL << 31)) return -1;   // the kernel counts rows in int32
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * wpb), lds, st, a, nt);
-  return check_launch("norm_rope_pipe_kernel");
-}
-
 // Launch of the pipelined rms_adaln kernel, one block of rows per CU.
 // Returns -1 (no launch) when the row does not fit its LDS plan.
 template <typename TX, bool WEIGHT, int N>
@@ -1173,15 +1188,44 @@ static int launch_adaln_pipe(RowArgs& a, hipStream_t st) {
   return -1;
 }
 
+#ifndef XMH3_COOP_ROWS
+#define XMH3_COOP_ROWS 4
+#endif
+// Launch of the cooperative norm-rope kernel: one block per CU of R rows of
+// D / 1024 waves (R * P <= 16, R <= 4). Returns -1 (no launch) when the row
+// does not fit it.
+template <typename TX, typename TF, bool ADALN, int P>
+static int launch_coop_p(RowArgs& a, int nt, hipStream_t st) {
+  const int R = std::max(1, std::min(XMH3_COOP_ROWS, 16 / P));
+  const size_t lds = (ADALN ? 8 * (size_t)a.D : 0) + (size_t)R * P * 2048 + (size_t)2 * R * 2 * P * 32 * 4 +
+                     2 * (size_t)R * 64 * 4 * sizeof(typename TF::storage);
+  if (lds > LDS_BYTES) return -1;
+  auto kern = norm_rope_coop_kernel<TX, TF, ADALN, P>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES) !=
+        hipSuccess)
+      return fail(XMH3_EHIP, "norm-rope kernel: cannot raise the dynamic LDS limit");
+    attr_set = true;
+  }
+  const int64_t cus = std::max(1, cu_count());
+  const int64_t grid = std::min<int64_t>((a.rows * nt + R - 1) / R, cus);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * P * R), lds, st, a, nt);
+  return check_launch("norm_rope_coop_kernel");
+}
+
 template <typename TX, typename TF, bool ADALN>
-static int launch_pipe(RowArgs& a, int nt, hipStream_t st) {
+static int launch_coop(RowArgs& a, int nt, hipStream_t st) {
   if (a.D % 1024 != 0) return -1;
   switch (a.D / 1024) {
-    case 1: return launch_pipe_n<TX, TF, ADALN, 1>(a, nt, st);
-    case 2: return launch_pipe_n<TX, TF, ADALN, 2>(a, nt, st);
-    case 3: return launch_pipe_n<TX, TF, ADALN, 3>(a, nt, st);
-    case 4: return launch_pipe_n<TX, TF, ADALN, 4>(a, nt, st);
-    case 5: return launch_pipe_n<TX, TF, ADALN, 5>(a, nt, st);
+    case 1: return launch_coop_p<TX, TF, ADALN, 1>(a, nt, st);
+    case 2: return launch_coop_p<TX, TF, ADALN, 2>(a, nt, st);
+    case 3: return launch_coop_p<TX, TF, ADALN, 3>(a, nt, st);
+    case 4: return launch_coop_p<TX, TF, ADALN, 4>(a, nt, st);
+    case 5: return launch_coop_p<TX, TF, ADALN, 5>(a, nt, st);
+    case 6: return launch_coop_p<TX, TF, ADALN, 6>(a, nt, st);
+    case 7: return launch_coop_p<TX, TF, ADALN, 7>(a, nt, st);
+    case 8: return launch_coop_p<TX, TF, ADALN, 8>(a, nt, st);
     default: return -1;
   }
 }
@@ -1212,14 +1256,14 @@ int norm_rope_rows(const void* x0, void* o0, const void* x1, void* o1, int dtype
   XMH3_REQUIRE(adaln == (shift != nullptr), "norm_rope: scale and shift go together");
   const size_t fsize = freqs_dtype == DT_F32 ? 4 : 2;
   XMH3_REQUIRE((freqs_row_stride * (int64_t)fsize) % 16 == 0, "norm_rope: table rows must be 16-byte aligned");
-  // one modulation row for every token (or none): the pipelined kernel
+  // one modulation row for every token (or none): the cooperative kernel
   const bool one_mod_row = !adaln || mod_group >= rows;
   const int nt = x1 ? 2 : 1;
 #define XMH3_NR(TX, TF)                                                         \
   {                                                                             \
     if (one_mod_row) {                                                          \
-      const int rc = adaln ? launch_pipe<TX, TF, true>(a, nt, st)               \
-                           : launch_pipe<TX, TF, false>(a, nt, st);             \
+      const int rc = adaln ? launch_coop<TX, TF, true>(a, nt, st)               \
+                           : launch_coop<TX, TF, false>(a, nt, st);             \
       if (rc >= 0) return rc;                                                   \
     }                                                                           \
     if (adaln) return launch_row<TX, TX, TF, true, true, false, 8>(a, st);      \
