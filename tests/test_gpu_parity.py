@@ -684,6 +684,12 @@ def test_rms_adaln(pkg, dev, mod_dtype):
     (300, 6144, ((0, 7, 0), (7, 150, 1), (150, 300, 2))),
     (300, 6152, ((0, 7, 0), (7, 150, 1), (150, 300, 2))),
     (257, 520, ((0, 3, 0), (3, 100, 1), (100, 257, 2))),
+    # cooperative plan (rows split over waves of 1024 elements): one i-step
+    # past the last full chunk (1056), a short last part with no partial
+    # chunk (2560), twelve parts and one row per block (11776)
+    (700, 1056, ((0, 50, 0), (50, 600, 1), (600, 700, 2))),
+    (500, 2560, ((0, 1, 0), (1, 499, 1), (499, 500, 2))),
+    (200, 11776, ((0, 13, 0), (13, 100, 1), (100, 200, 2))),
 ])
 def test_h3_segmented_rms_adaln(pkg, dev, rows, width, segs):
     say(f"h3 segmented rms_adaln rows={rows} width={width}")
@@ -699,6 +705,36 @@ def test_h3_segmented_rms_adaln(pkg, dev, rows, width, segs):
     want = cpu_ref.rms_adaln_segmented(x, w, sh, sc, segs, eps=1e-5)
     close(out, want, "segmented rms_adaln")
     assert same(out, want, "segmented rms_adaln")
+
+
+def test_h3_segmented_rms_adaln_many_iterations(pkg, dev):
+    """H3's width over enough rows that each block of the cooperative kernel
+    runs past 64 row groups, where its per-lane table of modulation rows is
+    refilled: the rows of iterations 62-66 of every block are checked against
+    the oracle (a window of the output, the oracle run on that window)."""
+    from x_minimaxh3_amd import h3
+
+    width, rows_per_group = 5376, 2                  # 6 waves of 1024 per row, 2 rows per block
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rows = 68 * cus * rows_per_group + 7             # 68 iterations, a partial last group
+    say(f"h3 segmented rms_adaln rows={rows} width={width} (modulation refill)")
+    g = torch.Generator().manual_seed(25)
+    x = torch.randn(rows, width, generator=g).to(torch.bfloat16)
+    w = (torch.rand(width, generator=g) + 0.5).to(torch.bfloat16)
+    sc = (torch.randn(3, width, generator=g) * 0.1).to(torch.bfloat16)
+    sh = (torch.randn(3, width, generator=g) * 0.1).to(torch.bfloat16)
+    lo, hi = 62 * cus * rows_per_group, 67 * cus * rows_per_group
+    cut = (lo + hi) // 2 + 3                         # a segment boundary inside the window
+    segs = ((0, 1000, 0), (1000, cut, 1), (cut, rows, 2))
+    out = h3.rms_adaln(x.to(dev), w.to(dev), sh.to(dev), sc.to(dev), segs, eps=1e-5)
+    torch.cuda.synchronize()
+    window = ((lo, cut, 1), (cut, hi, 2))
+    want = cpu_ref.rms_adaln_segmented(x[lo:hi], w, sh, sc, tuple((a - lo, b - lo, r) for a, b, r in window),
+                                       eps=1e-5)
+    got = out[lo:hi].cpu()
+    assert same(got, want, "segmented rms_adaln (iterations 62-66)")
+    tail = cpu_ref.rms_adaln_segmented(x[-300:], w, sh, sc, ((0, 300, 2),), eps=1e-5)
+    assert same(out[-300:].cpu(), tail, "segmented rms_adaln (last rows)")
 
 
 # --------------------------------------------------------------------------- token-chunked driver

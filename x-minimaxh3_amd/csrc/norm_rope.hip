@@ -838,6 +838,242 @@ __global__ __launch_bounds__(512) void adaln_pipe_kernel(RowArgs a, int64_t chun
 }
 
 // ---------------------------------------------------------------------------
+// Cooperative rms_adaln for 16-bit rows whose modulation has the rows'
+// dtype, on the plan of the cooperative norm-rope kernel: a row is split
+// into W parts of PS = 512 CPP elements (the last part may be shorter), one
+// wave per part; a block of R * W waves takes the R consecutive rows of a
+// row group per iteration, one block per CU, the blocks visiting groups
+// blockIdx.x, + gridDim.x, ... (one dense window of rows in flight).
+//
+// The reference-order sum of squares (ref_order_sumsq): full chunks j of 512
+// positions give chain sums c_j (16 squares from zero), folded in order into
+// the acc1 / acc2 / acc3 cascade; the rem = D / 32 - 16 * nchunks i-steps
+// past the last full chunk are summed from zero into acc0 (by the wave whose
+// part holds them: host-checked to be one part), and D % 32 == 0 leaves no
+// leftover vector. Each wave writes its chunk sums (and acc0), and after an
+// LDS-only barrier every wave of the row folds them in the reference order:
+// bit-identical rrms.
+//
+// Per lane: CPP items of 8 elements at part offsets 512 k + 8 lane (clamped
+// to the row's last item past the end, and rows past the last to the last
+// row: every load and store is unpredicated, a clamped item rewrites its
+// source item's identical output, computed from loads issued before any
+// store of that row group, so in-place calls stay exact), the norm weight of
+// those items held as fp32 for the whole kernel, round(1 + scale) and shift
+// of the current modulation row held as fp32 until a row of another
+// modulation row comes (segment or sample boundaries). PF row groups are
+// prefetched into registers. LDS: per wave a staged part (512-element blocks
+// padded by 64 bytes, so the two halves of a wave's ordered reads fall in
+// different banks), chunk sums and acc0 in two parity slots.
+//
+// The kernel is VALU-heavy for a streaming kernel (about 10 VALU operations
+// per element at 64 lanes per CU per clock): the modulation is unpacked once,
+// the last rounding is the output packing, and every memory operation is
+// issued on every path so that the compiler's waits leave the prefetch in
+// flight (a conditional load or store anywhere in the loop makes them wait
+// for everything).
+// ---------------------------------------------------------------------------
+template <typename TX, bool WEIGHT, int CPP, int PF>
+__global__ __launch_bounds__(768) void adaln_coop_kernel(RowArgs a, int W) {
+  using S = typename TX::storage;
+  static_assert(sizeof(S) == 2, "16-bit rows");
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int PS = 512 * CPP, SLICE = PS + 32 * CPP;      // staged elements per wave (padded)
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+  const int D = (int)a.D;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int R = (blockDim.x >> 6) / W;
+  const int sub = w / W, part = w - sub * W;
+  const int steps = D >> 5, nchunks = steps >> 4, rem = steps - nchunks * 16;
+  S* stage = reinterpret_cast<S*>(dyn_lds) + w * SLICE;
+  float* sums = reinterpret_cast<float*>(dyn_lds + (size_t)R * W * SLICE * sizeof(S));   // [2][R][nchunks][32]
+  float* acc0s = sums + 2 * R * nchunks * 32;                                              // [2][R][32]
+  const int base = part * PS;
+  const int last_item = D - 8;
+  auto col = [&](int k) { const int c = base + k * 512 + lane * 8; return c < D ? c : last_item; };
+  auto spos = [&](int p) { return p + (p >> 9) * 32; };     // padded staging position of part offset p
+
+  // weight, round(1 + scale) and shift held as fp32 (unpacked once)
+  float wf[CPP][8], tf[CPP][8], shf[CPP][8];
+  if constexpr (WEIGHT) {
+#pragma unroll
+    for (int k = 0; k < CPP; ++k) {
+      V8<TX> wv;
+      ld8<TX>(a.weight, col(k), wv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wf[k][j] = g8<TX>(wv, j);
+    }
+  }
+  int64_t mcur = -1;
+  auto load_mod = [&](int64_t m) __attribute__((always_inline)) {
+    const S* sc = static_cast<const S*>(a.scale) + m * a.mod_ld;
+    const S* sh = static_cast<const S*>(a.shift) + m * a.mod_ld;
+#pragma unroll
+    for (int k = 0; k < CPP; ++k) {
+      V8<TX> vs, vh;
+      ld8<TX>(sc, col(k), vs);
+      ld8<TX>(sh, col(k), vh);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        tf[k][j] = TX::round(1.0f + g8<TX>(vs, j));   // (1 + scale) in its dtype
+        shf[k][j] = g8<TX>(vh, j);
+      }
+    }
+    mcur = m;
+  };
+
+  // 32-bit row and group indices (the launcher checks rows < 2^30). The wave
+  // takes row gg * R + sub of groups gg = blockIdx.x + it * G, it = 0, 1, ...
+  const int nrows = (int)a.rows, ngroups = (nrows + R - 1) / R;
+  const int G = gridDim.x;
+  if ((int)blockIdx.x >= ngroups) return;   // uniform per block
+  const int iters = (ngroups - (int)blockIdx.x + G - 1) / G;
+  auto row_of = [&](int it) {
+    const int row = ((int)blockIdx.x + it * G) * R + sub;
+    return row < nrows ? row : nrows - 1;   // past the end: the last row again
+  };
+
+  // Modulation rows of this wave's rows, 64 iterations at a time: lane l
+  // holds that of iteration it0 + l. The refill consumes its load inside its
+  // branch, so no load of it is pending past the branch, and the loop's waits
+  // count only the row loads and stores.
+  int mtab = 0;
+  const int mod_group = (int)a.mod_group;   // < 2^31 (launcher)
+  auto fill = [&](int it0) __attribute__((always_inline)) {
+    const int row = row_of(it0 + lane < iters ? it0 + lane : iters - 1);
+    if (a.row_map) {
+      const int r = a.row_map[row];
+      mtab = r < 0 ? 0 : (r >= mod_group ? mod_group - 1 : r);   // clamped into the table
+    } else {
+      mtab = row / mod_group;
+    }
+  };
+
+  auto issue = [&](int it, u32x4 (&bx)[CPP]) __attribute__((always_inline)) {
+    const S* xb = static_cast<const S*>(a.x0) + (int64_t)row_of(it < iters ? it : iters - 1) * a.ldx;
+#pragma unroll
+    for (int k = 0; k < CPP; ++k)   // streamed once: non-temporal
+      bx[k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + col(k)));
+  };
+
+  int par = 0;
+  auto process = [&](int it, u32x4 (&bx)[CPP]) __attribute__((always_inline)) {
+    const int row = row_of(it);
+    const int slot = par * R + sub;
+#pragma unroll
+    for (int k = 0; k < CPP; ++k) *reinterpret_cast<u32x4*>(stage + spos(k * 512 + lane * 8)) = bx[k];
+    __builtin_amdgcn_sched_barrier(0);
+    issue(it + PF, bx);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's staging stores done
+    __builtin_amdgcn_wave_barrier();
+    {
+      const int L = lane & 31, h = lane >> 5;
+#pragma unroll
+      for (int q = 0; q < CPP; q += 2) {
+        const int j = part * CPP + q + h;                     // this lane's chunk
+        if (q + h < CPP && j < nchunks) {
+          float c = 0.0f;
+#pragma unroll
+          for (int u = 0; u < 16; ++u) c = add_sq<TX>(c, TX::load(stage[(q + h) * 544 + u * 32 + L]));
+          sums[(slot * nchunks + j) * 32 + L] = c;
+        }
+      }
+      if (rem && base <= nchunks * 512 && nchunks * 512 < base + PS && h == 0) {
+        // the i-steps past the last full chunk (this part holds them)
+        float c0 = 0.0f;
+        const int p0 = nchunks * 512 - base;
+        const S* rp = stage + spos(p0) + L;   // one 512-element block
+        for (int i = 0; i < rem; ++i) c0 = add_sq<TX>(c0, TX::load(rp[i * 32]));
+        acc0s[slot * 32 + L] = c0;
+      }
+    }
+    // publish the sums to the block (LDS only: the prefetched rows stay in flight)
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_barrier" ::: "memory");
+    float rr;
+    {
+      const int L = lane & 31;
+      const float* cs = sums + slot * nchunks * 32 + L;
+      float acc1 = 0.0f, acc2 = 0.0f, acc3 = 0.0f;
+      for (int j = 0; j < nchunks; ++j) {
+        acc1 = acc1 + cs[j * 32];
+        const int i_end = (j + 1) * 16;
+        if ((i_end & (15 << 4)) == 0) {
+          acc2 = acc2 + acc1;
+          acc1 = 0.0f;
+          if ((i_end & (15 << 8)) == 0) {
+            acc3 = acc3 + acc2;
+            acc2 = 0.0f;
+          }
+        }
+      }
+      const float acc0 = rem ? acc0s[slot * 32 + L] : 0.0f;
+      const float tot = ((acc0 + acc1) + acc2) + acc3;
+      const int v8 = lane & 7;
+      const float r0 = __shfl(tot, v8, 64), r1 = __shfl(tot, v8 + 8, 64);
+      const float r2 = __shfl(tot, v8 + 16, 64), r3 = __shfl(tot, v8 + 24, 64);
+      const float pv = ((r0 + r1) + r2) + r3;
+      float fin = 0.0f;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) fin = fin + __shfl(pv, v, 64);
+      rr = 1.0f / sqrtf(fin / (float)D + a.eps);
+    }
+    if ((it & 63) == 0) fill(it);
+    const int64_t m = __builtin_amdgcn_readlane(mtab, it & 63);
+    if (m != mcur) load_mod(m);
+    S* ob = static_cast<S*>(a.o0) + (int64_t)row * a.ldo;
+#pragma unroll
+    for (int k = 0; k < CPP; ++k) {
+      V8<TX> xv;
+      xv.v = *reinterpret_cast<const uint4*>(stage + spos(k * 512 + lane * 8));
+      float y[8];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        float n0 = g8<TX>(xv, j) * rr, n1 = g8<TX>(xv, j + 1) * rr;
+        if constexpr (WEIGHT) { n0 = n0 * wf[k][j]; n1 = n1 * wf[k][j + 1]; }
+        TX::round2(n0, n1);
+        n0 = n0 * tf[k][j]; n1 = n1 * tf[k][j + 1];
+        TX::round2(n0, n1);
+        y[j] = n0 + shf[k][j];          // the packing below is its rounding
+        y[j + 1] = n1 + shf[k][j + 1];
+      }
+      const V8<TX> ov = pack8<TX>(y);
+      // unpredicated: a clamped item (past the row's end, or a row past the
+      // last) rewrites its source item's output with identical bytes
+      __builtin_nontemporal_store(u32x4{ov.v.x, ov.v.y, ov.v.z, ov.v.w}, reinterpret_cast<u32x4*>(ob + col(k)));
+    }
+    // the next row's staging overwrites this wave's slice
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    par ^= 1;
+  };
+
+  // PF groups in flight, in PF register buffers taken in turn (iteration it
+  // in buffer it % PF). The first iteration is peeled off the loop, the loop
+  // body is PF whole iterations with its only exit at the bottom and the
+  // last (iters - 1) % PF iterations follow it: the loop head is then reached
+  // only with the other buffers' loads, one prefetch and its stores
+  // outstanding (as on the back edge, save for older stores), so the waits
+  // the compiler places there leave the prefetched groups in flight.
+  u32x4 xb[PF][CPP];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) issue(i, xb[i]);
+  __builtin_amdgcn_sched_barrier(0);
+  process(0, xb[0]);
+  int it = 1;
+  for (; it + PF <= iters; it += PF) {
+#pragma unroll
+    for (int i = 1; i <= PF; ++i) process(it + i - 1, xb[i % PF]);
+  }
+#pragma unroll
+  for (int i = 1; i < PF; ++i)
+    if (it + i - 1 < iters) process(it + i - 1, xb[i % PF]);
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): no load lands after the wave ends
+}
+
+// ---------------------------------------------------------------------------
 // head-span kernel: LPH lanes per (b, s, h) head
 // ---------------------------------------------------------------------------
 // Division of non-negative 64-bit values by a launch-invariant divisor d >= 1
@@ -1177,6 +1413,44 @@ static int launch_adaln_pipe_n(RowArgs& a, hipStream_t st) {
   return check_launch("adaln_pipe_kernel");
 }
 
+#ifndef XMH3_ADALN_CPP
+#define XMH3_ADALN_CPP 2
+#endif
+#ifndef XMH3_ADALN_PF
+#define XMH3_ADALN_PF 2
+#endif
+// Launch of the cooperative rms_adaln kernel: one block per CU of R rows of
+// W = ceil(D / PS) waves (R * W <= 12). Returns -1 (no launch) when the row
+// does not fit its plan (D % 32, the i-steps past the last full chunk split
+// over two parts, LDS).
+template <typename TX, bool WEIGHT>
+static int launch_adaln_coop(RowArgs& a, hipStream_t st) {
+  constexpr int CPP = XMH3_ADALN_CPP, PS = 512 * CPP, PF = XMH3_ADALN_PF;
+  if (a.x1 || a.D % 32 != 0 || a.D > 16384 || a.rows >= (int64_t(1) << 30) ||
+      a.mod_group >= (int64_t(1) << 31))
+    return -1;
+  const int D = (int)a.D, W = (D + PS - 1) / PS;
+  const int nchunks = D / 512, rem = D / 32 - nchunks * 16;
+  if (rem && (nchunks * 512) / PS != (D - 1) / PS) return -1;
+  if (W > 12) return -1;
+  const int R = std::max(1, 12 / W);
+  const size_t lds = (size_t)R * W * (PS + 32 * CPP) * sizeof(typename TX::storage) +
+                     (size_t)2 * R * nchunks * 32 * 4 + (size_t)2 * R * 32 * 4;
+  if (lds > LDS_BYTES) return -1;
+  auto kern = adaln_coop_kernel<TX, WEIGHT, CPP, PF>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_BYTES) !=
+        hipSuccess)
+      return fail(XMH3_EHIP, "rms_adaln kernel: cannot raise the dynamic LDS limit");
+    attr_set = true;
+  }
+  const int64_t cus = std::max(1, cu_count());
+  const int64_t grid = std::min<int64_t>((a.rows + R - 1) / R, cus);
+  hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * W * R), lds, st, a, W);
+  return check_launch("adaln_coop_kernel");
+}
+
 template <typename TX, bool WEIGHT>
 static int launch_adaln_pipe(RowArgs& a, hipStream_t st) {
   if (a.x1 || a.D % 8 != 0 || a.D >= (1 << 17)) return -1;
@@ -1296,7 +1570,9 @@ int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D,
   a.scale = scale; a.shift = shift; a.mod_ld = mod_ld; a.row_map = row_map; a.mod_group = mod_group;
   a.eps = eps;
   if (dtype == DT_BF16 && mod_dtype == DT_BF16) {
-    const int rc = weight ? launch_adaln_pipe<BF16T, true>(a, st) : launch_adaln_pipe<BF16T, false>(a, st);
+    int rc = weight ? launch_adaln_coop<BF16T, true>(a, st) : launch_adaln_coop<BF16T, false>(a, st);
+    if (rc != -1) return rc;
+    rc = weight ? launch_adaln_pipe<BF16T, true>(a, st) : launch_adaln_pipe<BF16T, false>(a, st);
     if (rc != -1) return rc;
   }
 #define XMH3_RA(TX, TM)                                                          \
