@@ -506,10 +506,17 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
   }
   __syncthreads();
 
-  const int64_t ntok = a.rows, nrows = ntok * nt, ngroups = (nrows + R - 1) / R;
-  const int64_t G = gridDim.x;
-  int64_t g = blockIdx.x;
-  if (g >= ngroups) return;   // uniform per block
+  // 32-bit row and group indices (the launcher checks rows * nt < 2^30); the
+  // wave takes row gg * R + sub of groups gg = blockIdx.x + it * G
+  const int ntok = (int)a.rows, nrows = ntok * nt, ngroups = (nrows + R - 1) / R;
+  const int G = gridDim.x;
+  if ((int)blockIdx.x >= ngroups) return;   // uniform per block
+  const int iters = (ngroups - (int)blockIdx.x + G - 1) / G;
+  auto row_of = [&](int it) {
+    it = it < iters ? it : iters - 1;       // past the block's last iteration: that one again
+    const int row = ((int)blockIdx.x + it * G) * R + sub;
+    return row < nrows ? row : nrows - 1;   // past the end: the last row again
+  };
 
   const int qh = lane / IPH, it8 = (lane % IPH) * 8;
   const int o0 = part * 1024 + qh * HD + it8;                         // item 0; item 1 at + 64
@@ -520,28 +527,30 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
   // lanes of one 8-pair group read consecutive slots
   const int tab_slot = (tab_lane % CPG) * IPH + tab_lane / CPG;
 
-  // this wave's row in group gg; past the end, the last row is read again
-  // (computed, never stored) so every wave keeps the block's barriers
-  auto issue = [&](int64_t gg, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
-    int64_t row = gg * R + sub;
-    row = row < nrows ? row : nrows - 1;
-    const int64_t tok = row < ntok ? row : row - ntok;
-    const S* xb = static_cast<const S*>(row < ntok ? a.x0 : a.x1) + tok * a.ldx + o0;
+  // this wave's row of iteration it; rows past the last are the last row
+  // again, computed from loads issued before any store of their row group and
+  // stored with identical bytes (so in-place calls stay exact), so that every
+  // wave keeps the block's barriers and issues the same memory operations on
+  // every path (the compiler's waits then leave the prefetch in flight)
+  auto issue = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
+    const int row = row_of(it);
+    const int tok = row < ntok ? row : row - ntok;
+    const S* xb = static_cast<const S*>(row < ntok ? a.x0 : a.x1) + (int64_t)tok * a.ldx + o0;
     bx[0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb));
     bx[1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(xb + HD / 2));
-    const SF* tb = static_cast<const SF*>(a.freqs) + (a.freqs_row_stride ? tok * a.freqs_row_stride : 0);
+    const SF* tb = static_cast<const SF*>(a.freqs) + (a.freqs_row_stride ? (int64_t)tok * a.freqs_row_stride : 0);
     bt = *reinterpret_cast<const u32x4*>(tb + tab_lane * EPC);
   };
 
   int par = 0;
-  auto process = [&](int64_t gg, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
-    const int64_t row = gg * R + sub;
+  auto process = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
+    const int row = row_of(it);
     const int slot = par * R + sub;
     *reinterpret_cast<u32x4*>(stage + sl0) = bx[0];
     *reinterpret_cast<u32x4*>(stage + sl1) = bx[1];
     if (part == 0 && lane < TAB_CHUNKS) tabs[slot * TAB_CHUNKS + tab_slot] = bt;
     __builtin_amdgcn_sched_barrier(0);
-    issue(gg + 2 * G, bx, bt);
+    issue(it + 2, bx, bt);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's staging stores done
     __builtin_amdgcn_wave_barrier();
@@ -649,9 +658,9 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
       w0[j >> 1] = TX::store2(q0[0], q0[1]);
       w1[j >> 1] = TX::store2(q1[0], q1[1]);
     }
-    if (row < nrows) {
-      const int64_t tok = row < ntok ? row : row - ntok;
-      S* ob = static_cast<S*>(row < ntok ? a.o0 : a.o1) + tok * a.ldo + o0;
+    {
+      const int tok = row < ntok ? row : row - ntok;
+      S* ob = static_cast<S*>(row < ntok ? a.o0 : a.o1) + (int64_t)tok * a.ldo + o0;
       __builtin_nontemporal_store(u32x4{w0[0], w0[1], w0[2], w0[3]}, reinterpret_cast<u32x4*>(ob));
       __builtin_nontemporal_store(u32x4{w1[0], w1[1], w1[2], w1[3]}, reinterpret_cast<u32x4*>(ob + HD / 2));
     }
@@ -661,21 +670,24 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
     par ^= 1;
   };
 
-  // the first group is peeled off the loop so that the loop is entered with
-  // the same loads outstanding as on its back edge: the compiler's wait
-  // counts then leave the second prefetched group in flight
+  // Two row groups in flight, in two register buffers taken in turn. The
+  // first iteration is peeled off the loop and the loop body is two whole
+  // iterations with its only exit at the bottom: the loop head is then
+  // reached only with the other buffer's loads, one prefetch and its stores
+  // outstanding, as on the back edge, so the compiler's waits there leave the
+  // prefetched group in flight (a loop with an exit between its two halves
+  // gives the head a path with fewer operations outstanding, and the waits
+  // then drain the prefetch). An odd count ends with one extra iteration
+  // that redoes the block's last one: its loads were issued before that
+  // iteration's stores, so it stores identical bytes, also in place.
   u32x4 x0[2], x1[2], t0, t1;
-  issue(g, x0, t0);
-  issue(g + G, x1, t1);
+  issue(0, x0, t0);
+  issue(1, x1, t1);
   __builtin_amdgcn_sched_barrier(0);
-  process(g, x0, t0);
-  g += G;
-  while (g < ngroups) {
-    process(g, x1, t1);
-    g += G;
-    if (g >= ngroups) break;
-    process(g, x0, t0);
-    g += G;
+  process(0, x0, t0);
+  for (int it = 1; it < iters; it += 2) {
+    process(it, x1, t1);
+    process(it + 1, x0, t0);
   }
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): no load lands after the wave ends
 }
@@ -1470,6 +1482,7 @@ static int launch_adaln_pipe(RowArgs& a, hipStream_t st) {
 // does not fit it.
 template <typename TX, typename TF, bool ADALN, int P>
 static int launch_coop_p(RowArgs& a, int nt, hipStream_t st) {
+  if (a.rows * nt >= (int64_t(1) << 30)) return -1;   // 32-bit row indices
   const int R = std::max(1, std::min(XMH3_COOP_ROWS, 16 / P));
   const size_t lds = (ADALN ? 8 * (size_t)a.D : 0) + (size_t)R * P * 2048 + (size_t)2 * R * 2 * P * 32 * 4 +
                      2 * (size_t)R * 64 * 4 * sizeof(typename TF::storage);
