@@ -1347,6 +1347,199 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Cooperative per-head RMSNorm + full split-half rotation of [B, S, H, D]
+// heads (the QK norm-rope), D = 64, 96 or 128, 16-bit values, one table row
+// per token (head stride 0). A token row of H heads is split into P parts of
+// HPW = 64 / LPH heads (LPH = D / 16 lanes per head, lane p holding the items
+// at head offsets 8 p and 8 p + D / 2; lanes past HPW * LPH, and the heads
+// past H of the last part, redo the part's last head), one wave per part; a
+// block of R * P waves takes R consecutive tokens per iteration, one block
+// per CU, the blocks visiting token groups blockIdx.x, + gridDim.x, ...: one
+// dense window of the tensor in flight, as in the cooperative norm-rope.
+// Wave p of a token loads the p-th slice of the token's table row, the block
+// shares the row in LDS (one LDS-only barrier per iteration, the table in
+// two parity slots), so each row is read once per token rather than once per
+// wave. The sum of squares of a head stays in its wave: HPW x 8 jobs, job
+// (head, v) summing the chains v, v + 8, v + 16, v + 24 (each D / 32 squares
+// from zero, the reference order of ref_order_sumsq with no full chunk and
+// no leftover vector) into ((c_v + c_v+8) + c_v+16) + c_v+24, and a head's
+// lanes add its 8 job results in order from zero: bit-identical rrms.
+// Every path issues the same loads and stores (clamped rows, heads and
+// iterations recompute from loads issued before any store of theirs and
+// store identical bytes, so in-place calls stay exact).
+// ---------------------------------------------------------------------------
+template <typename TX, typename TW, typename TF, int D>
+__global__ __launch_bounds__(768) void qk_coop_kernel(HeadArgs a, int P) {
+  using S = typename TX::storage;
+  using SF = typename TF::storage;
+  static_assert(sizeof(S) == 2, "16-bit heads");
+  static_assert(D == 64 || D == 96 || D == 128, "head width");
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int LPH = D / 16, HPW = 64 / LPH, HALF = D / 2, STEPS = D / 32;
+  constexpr int HROW = D + 8;                         // staged head (elements), rows 16 bytes apart in banks
+  constexpr int RB = HALF * 4 * (int)sizeof(SF);      // table row bytes
+  constexpr int RCH = RB / 16;                        // its 16-byte chunks
+  constexpr int NJOB = HPW * 8;
+  constexpr int WSLICE = HPW * HROW * 2 + NJOB * 4;   // LDS bytes per wave
+  extern __shared__ __attribute__((aligned(16))) uint8_t dyn_lds[];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int R = (blockDim.x >> 6) / P;
+  const int sub = w / P, part = w - sub * P;
+  S* xs = reinterpret_cast<S*>(dyn_lds + w * WSLICE);                 // [HPW][HROW]
+  float* rs = reinterpret_cast<float*>(dyn_lds + w * WSLICE + HPW * HROW * 2);
+  uint8_t* tabs = dyn_lds + R * P * WSLICE;                            // [2][R][RB]
+  const int slot0 = lane / LPH, p = lane - slot0 * LPH;
+  const int c0 = 8 * p, c1 = c0 + HALF;
+  // the lane's head within the token (past the part or the token: the last)
+  const int hl = min(part * HPW + min(slot0, HPW - 1), (int)a.H - 1);
+  const int hslot = hl - part * HPW;                                   // its staged row
+  const int cpw = (RCH + P - 1) / P;                                   // table chunks per wave
+  const int tch = min(part * cpw + min(lane, cpw - 1), RCH - 1);       // this lane's chunk
+  // Global loads and stores move whole 16-byte chunks in memory order (lane
+  // l: chunks l and 64 + l of the part, CPH per head), so each instruction
+  // covers whole cache lines; the pairs are formed in LDS. Chunks past the
+  // part's heads (or past H) redo the part's last chunk.
+  constexpr int CPH = D / 8, NCHK = HPW * CPH;
+  int ch_head[2], ch_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = min(lane + 64 * i, NCHK - 1);
+    const int hh = min(part * HPW + c / CPH, (int)a.H - 1);
+    ch_head[i] = hh;
+    ch_off[i] = (hh - part * HPW) * HROW + (hh == part * HPW + c / CPH ? c % CPH : CPH - 1) * 8;
+  }
+
+  float w0[8], w1[8];          // the lane's norm weights
+  {
+    V8<TW> v0, v1;
+    ld8<TW>(a.weight, c0, v0);
+    ld8<TW>(a.weight, c1, v1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { w0[j] = g8<TW>(v0, j); w1[j] = g8<TW>(v1, j); }
+  }
+
+  // 32-bit token indices (the launcher checks B S < 2^30)
+  const int ntok = (int)(a.B * a.S), ngroups = (ntok + R - 1) / R;
+  const int G = gridDim.x;
+  if ((int)blockIdx.x >= ngroups) return;   // uniform per block
+  const int iters = (ngroups - (int)blockIdx.x + G - 1) / G;
+  // token of this wave in iteration it (past the block's last iteration:
+  // that one again; past the last token: the last token)
+  auto tok_of = [&](int it) {
+    it = it < iters ? it : iters - 1;
+    const int t = ((int)blockIdx.x + it * G) * R + sub;
+    return t < ntok ? t : ntok - 1;
+  };
+  struct Tok { int64_t x, o; const uint8_t* t; };
+  auto tok_at = [&](int t) __attribute__((always_inline)) {
+    const int64_t b = (int64_t)a.divS.div((uint64_t)t), s = (int64_t)t - b * a.S;
+    Tok r;
+    r.x = b * a.sb + s * a.ss;
+    r.o = b * a.ob + s * a.os;
+    r.t = static_cast<const uint8_t*>(a.freqs) + (b * a.fb + s * a.fs) * (int64_t)sizeof(SF);
+    return r;
+  };
+
+  auto issue = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
+    const Tok tk = tok_at(tok_of(it));
+    const S* xp = static_cast<const S*>(a.x) + tk.x;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      bx[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          xp + (int64_t)ch_head[i] * a.sh + (ch_off[i] - (ch_head[i] - part * HPW) * HROW)));
+    bt = *reinterpret_cast<const u32x4*>(tk.t + tch * 16);
+  };
+
+  int par = 0;
+  auto process = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
+    uint8_t* trow = tabs + (par * R + sub) * RB;
+    *reinterpret_cast<u32x4*>(&xs[ch_off[0]]) = bx[0];
+    *reinterpret_cast<u32x4*>(&xs[ch_off[1]]) = bx[1];
+    *reinterpret_cast<u32x4*>(trow + tch * 16) = bt;
+    __builtin_amdgcn_sched_barrier(0);
+    issue(it + 2, bx, bt);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the staging stores are done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = 0; q < (NJOB + 63) / 64; ++q) {
+      const int j = lane + 64 * q;
+      if (j < NJOB) {
+        const S* hr = xs + (j >> 3) * HROW;
+        const int v = j & 7;
+        float r = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float c = 0.0f;
+#pragma unroll
+          for (int i = 0; i < STEPS; ++i) c = add_sq<TX>(c, TX::load(hr[i * 32 + v + 8 * g]));
+          r = g ? r + c : c;
+        }
+        rs[j] = r;
+      }
+    }
+    // publish the job results and the table slices (LDS only: the
+    // prefetched rows stay in flight)
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("s_barrier" ::: "memory");
+    float fin = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) fin = fin + rs[hslot * 8 + v];
+    const float rr = 1.0f / sqrtf(fin / (float)D + a.eps);
+    V8<TX> v0, v1;
+    v0.v = *reinterpret_cast<const uint4*>(&xs[hslot * HROW + c0]);
+    v1.v = *reinterpret_cast<const uint4*>(&xs[hslot * HROW + c1]);
+    const SF* tp = reinterpret_cast<const SF*>(trow) + c0 * 4;   // pair c0's entries
+    float r0[8], r1[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float y0 = TX::round((g8<TX>(v0, j) * rr) * w0[j]);
+      const float y1 = TX::round((g8<TX>(v1, j) * rr) * w1[j]);
+      rotate_pair<TF, F32T>(y0, y1, TF::load(tp[4 * j]), TF::load(tp[4 * j + 1]), TF::load(tp[4 * j + 2]),
+                            TF::load(tp[4 * j + 3]), r0[j], r1[j]);
+    }
+    // the rotated pairs back into the staged heads, then out in memory order
+    const V8<TX> o0 = pack8<TX>(r0), o1 = pack8<TX>(r1);
+    *reinterpret_cast<uint4*>(&xs[hslot * HROW + c0]) = o0.v;
+    *reinterpret_cast<uint4*>(&xs[hslot * HROW + c1]) = o1.v;
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    const Tok tk = tok_at(tok_of(it));
+    S* op = static_cast<S*>(a.out) + tk.o;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4*>(&xs[ch_off[i]]);
+      __builtin_nontemporal_store(u32x4{v.x, v.y, v.z, v.w},
+                                  reinterpret_cast<u32x4*>(op + (int64_t)ch_head[i] * a.oh +
+                                                           (ch_off[i] - (ch_head[i] - part * HPW) * HROW)));
+    }
+    // the next token's staging overwrites the wave's slice
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    par ^= 1;
+  };
+
+  // Two token groups in flight in two register buffers taken in turn: the
+  // first iteration is peeled off, the loop body is two whole iterations
+  // with its only exit at the bottom (an odd count ends with a redo of the
+  // block's last iteration, whose loads precede that iteration's stores), so
+  // the loop head is reached only with one buffer's loads, one prefetch and
+  // its stores outstanding and the compiler's waits leave the prefetch in
+  // flight.
+  u32x4 x0[2], x1[2], t0, t1;
+  issue(0, x0, t0);
+  issue(1, x1, t1);
+  __builtin_amdgcn_sched_barrier(0);
+  process(0, x0, t0);
+  for (int it = 1; it < iters; it += 2) {
+    process(it, x1, t1);
+    process(it + 1, x0, t0);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): no load lands after the wave ends
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 template <typename TX, typename TM, typename TF, bool ROPE, bool ADALN, bool WEIGHT, int IPH, int N>
@@ -1602,9 +1795,38 @@ int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D,
   return fail(XMH3_EUNSUPPORTED, "rms_adaln: dtype combination not supported");
 }
 
+// Launch of the cooperative QK norm-rope when it serves the call (full
+// rotation of 64-, 96- or 128-wide heads, one table row per token, at most 12
+// parts per token); -1 otherwise.
+template <typename TX, typename TW, typename TF>
+static int launch_qk_coop(HeadArgs& a, hipStream_t st) {
+  const int64_t ntok = a.B * a.S;
+  if (a.rot != a.D || a.fh != 0 || ntok >= (int64_t(1) << 30)) return -1;
+  auto go = [&](auto kern, int D) -> int {
+    const int lph = D / 16, hpw = 64 / lph;
+    const int P = (int)((a.H + hpw - 1) / hpw);
+    if (P > 12) return -1;
+    const int R = std::max(1, 12 / P);
+    const size_t wslice = (size_t)hpw * (D + 8) * 2 + (size_t)hpw * 8 * 4;
+    const size_t rb = (size_t)(D / 2) * 4 * sizeof(typename TF::storage);
+    const size_t lds = (size_t)R * P * wslice + 2 * (size_t)R * rb;
+    if (lds > LDS_BYTES) return -1;
+    const int64_t grid = std::min<int64_t>((ntok + R - 1) / R, std::max(1, cu_count()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * P * R), lds, st, a, P);
+    return check_launch("qk_coop_kernel");
+  };
+  if (a.D == 64) return go(qk_coop_kernel<TX, TW, TF, 64>, 64);
+  if (a.D == 96) return go(qk_coop_kernel<TX, TW, TF, 96>, 96);
+  if (a.D == 128) return go(qk_coop_kernel<TX, TW, TF, 128>, 128);
+  return -1;
+}
+
 template <typename TX, typename TW, typename TF, bool NORM, bool SPLIT>
 static int launch_head(HeadArgs& a, int lph, hipStream_t st) {
   const int64_t nheads = a.B * a.S * a.H;
+  if constexpr (NORM && SPLIT && sizeof(typename TX::storage) == 2) {
+    if (const int rc = launch_qk_coop<TX, TW, TF>(a, st); rc != -1) return rc;
+  }
   // table rows through LDS: shared by the heads of a token, at most
   // HEAD_TAB_ROWS tokens per block, rows of at most HEAD_TAB_ROW_BYTES
   auto tabl_ok = [&](int L) {
