@@ -117,18 +117,22 @@ def cpu_baseline_norm_rope(nr: dict, repeats: int = 3) -> dict:
             "kind": "port", "cpu_model": host_cpu_model(), "sample": f"oracle norm_rope on Q and K, full {m}x{d}, median of {repeats}"}
 
 
-def settle(fn, min_s: float = 0.3) -> None:
-    """Run `fn` untimed for at least `min_s` seconds before its warm-up steps.
-    An MI355X that has been idle (input generation, a host-side phase) takes
-    tens of milliseconds of sustained load to bring its clocks back up: in a
-    kernel trace of this bench the 720p fc1 GEMM ran 1.86, 1.63, 1.52 ... ms
-    over its first launches and settled at 1.37 ms after about twelve."""
+def settle(fn, min_s: float = 0.5) -> None:
+    """Run `fn` untimed for at least `min_s` seconds before its warm-up steps,
+    in batches of launches queued back to back. An MI355X that has been idle
+    (input generation, a host-side phase) takes tens of milliseconds of
+    sustained load to bring its clocks back up: in a kernel trace of this
+    bench the 720p fc1 GEMM ran 1.86, 1.63, 1.52 ... ms over its first
+    launches and settled at 1.37 ms after about twelve, and the H3 QK
+    rms_rope on freshly allocated tensors took about 100 ms of unbroken
+    launches to go from 360 us to its steady 200 us (short batches with a
+    synchronisation between them did not get it there)."""
     import torch
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < min_s:
-        for _ in range(4):
+        for _ in range(32):
             fn()
         torch.cuda.synchronize()
 

@@ -312,14 +312,33 @@ int xmh3_rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t
                     int rot_dim, float eps, int norm, int split_half, xmh3_stream_t stream);
 
 /*
+ * xmh3_rope_heads of Q and K [B, S, H, head_dim] with one table, each with
+ * its own strides, output and norm weight (both of weight_dtype). When the
+ * two tensors share strides (and outputs share strides), the per-head norm
+ * and full split-half rotation (norm = 1, split_half = 1, rot_dim 0 or
+ * head_dim, head_dim 64, 96 or 128, 16-bit values, the table shared by a
+ * token's heads) run in one launch over the rows of Q then K; otherwise one
+ * xmh3_rope_heads call per tensor. Outputs may alias their inputs.
+ * Replaces: CK/backends/cuda/ops/rms_rope.cu:353-384 launch_rms_rope_kernel
+ *   (q and k in one call); eager CK/backends/eager/rope.py:129-143,178-189
+ *   (rms_rope_split_half, rms_rope_split_half_).
+ */
+int xmh3_rope_heads_qk(void* q, void* q_out, void* k, void* k_out, int dtype, int64_t B, int64_t S, int64_t H,
+                       int64_t head_dim, const int64_t* q_strides, const int64_t* q_out_strides,
+                       const int64_t* k_strides, const int64_t* k_out_strides, const void* q_weight,
+                       const void* k_weight, int weight_dtype, const void* freqs, int freqs_dtype,
+                       const int64_t* freqs_strides, int rot_dim, float eps, int norm, int split_half,
+                       xmh3_stream_t stream);
+
+/*
  * The reference's per-head RMSNorm + RoPE launcher under its own name and
  * 46-argument list (7 pointers; batch, dim1, dim2, head_dim, rot_dim; the
  * table's three leading sizes; 4 strides each of q, k, q_out, k_out; 6 table
  * strides; the q / k weight strides; epsilon; input, table and weight dtype
  * codes; has_k; split_half; stream), so a ctypes caller with pinned argtypes
  * (h3serve/native_engine/model/single_qknorm_rope.py:36-66,158-187) binds
- * this library unchanged. Runs the head-span kernel of xmh3_rope_heads in
- * either pair layout. Returns nothing, as the reference does: an argument
+ * this library unchanged. Runs the kernels of xmh3_rope_heads_qk (q and k
+ * with norm weights) or xmh3_rope_heads in either pair layout. Returns nothing, as the reference does: an argument
  * outside this build's support (a strided head dimension, weight or table
  * pair layout) launches nothing and sets xmh3_last_error().
  * Replaces: CK/backends/cuda/ops/rms_rope.cu:353-384 launch_rms_rope_kernel.

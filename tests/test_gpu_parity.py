@@ -599,6 +599,36 @@ def test_rope_table_paths(pkg, dev, heads, per_head_table):
     assert same(k2, cpu_ref.rms_rope_split_half1(xk, tab, kw, 1e-5, D), "k")
 
 
+@pytest.mark.parametrize("S,H,D,tdtype,wdtype,dtype,inplace", [
+    (3001, 56, 96, torch.float32, torch.bfloat16, torch.bfloat16, True),    # H3 heads, many iterations
+    (517, 24, 64, torch.bfloat16, torch.float32, torch.bfloat16, False),
+    (389, 40, 128, torch.float32, torch.bfloat16, torch.bfloat16, True),
+    (211, 30, 96, torch.float16, torch.float16, torch.float16, False),
+    (5, 7, 96, torch.float32, torch.bfloat16, torch.bfloat16, True),        # fewer heads than a part holds
+])
+def test_qk_rope_pair_launch(pkg, dev, S, H, D, tdtype, wdtype, dtype, inplace):
+    """Q and K through one call of the pair entry (one launch of the
+    cooperative QK kernel when the strides match): full split-half rotation
+    with per-head RMSNorm, distinct Q and K weights, against the oracle bit
+    for bit."""
+    say(f"qk rope pair S={S} H={H} D={D} table={tdtype} weight={wdtype} {dtype} inplace={inplace}")
+    g = torch.Generator().manual_seed(S + H + D)
+    xq = torch.randn(1, S, H, D, generator=g).to(dtype)
+    xk = torch.randn(1, S, H, D, generator=g).to(dtype)
+    tab = _angle_table((1, S, 1), D // 2, S + 1, tdtype)
+    qw = (torch.rand(D, generator=g) + 0.5).to(wdtype)
+    kw = (torch.rand(D, generator=g) + 0.5).to(wdtype)
+    q2, k2 = xq.to(dev), xk.to(dev)
+    if inplace:
+        pkg.rms_rope_split_half_(q2, k2, tab.to(dev), qw.to(dev), kw.to(dev), 1e-5, 0)
+        oq, ok = q2, k2
+    else:
+        oq, ok = pkg.rms_rope_split_half(q2, k2, tab.to(dev), qw.to(dev), kw.to(dev), 1e-5, 0)
+    torch.cuda.synchronize()
+    assert same(oq, cpu_ref.rms_rope_split_half1(xq, tab, qw, 1e-5, 0), "q")
+    assert same(ok, cpu_ref.rms_rope_split_half1(xk, tab, kw, 1e-5, 0), "k")
+
+
 def test_h3_qknorm_rope_partial_inplace(pkg, dev):
     """H3 call form: per-head RMSNorm with weight, eps 1e-5, partial rotary 96
     of 128 with a bf16 table, in place on views of a packed QKV tensor."""

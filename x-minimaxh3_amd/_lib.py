@@ -70,6 +70,9 @@ SIGNATURES: dict[str, tuple] = {
                                      c_void_p, c_int, c_void_p, c_int, P_I64, c_int, c_float, c_int, c_void_p]),
     "xmh3_rope_heads": (c_int, [c_void_p, c_void_p, c_int, c_i64, c_i64, c_i64, c_i64, P_I64, P_I64,
                                 c_void_p, c_int, c_void_p, c_int, P_I64, c_int, c_float, c_int, c_int, c_void_p]),
+    "xmh3_rope_heads_qk": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_i64, c_i64, c_i64, c_i64,
+                                   P_I64, P_I64, P_I64, P_I64, c_void_p, c_void_p, c_int, c_void_p, c_int, P_I64,
+                                   c_int, c_float, c_int, c_int, c_void_p]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -1123,6 +1123,10 @@ struct HeadArgs {
   int64_t fb, fs, fh;                 // table strides (0 = broadcast), pairs contiguous
   int rot;                            // rotated prefix
   float eps;
+  // a second tensor of the same shape and strides (the cooperative QK
+  // kernel, nt = 2): its input, output and norm weight
+  void* x1; void* out1;
+  const void* weight1;
 };
 
 // TABL: the table is shared by the heads of a token (head stride 0) and the
@@ -1369,7 +1373,7 @@ __global__ __launch_bounds__(256) void headspan_kernel(HeadArgs a) {
 // store identical bytes, so in-place calls stay exact).
 // ---------------------------------------------------------------------------
 template <typename TX, typename TW, typename TF, int D>
-__global__ __launch_bounds__(768) void qk_coop_kernel(HeadArgs a, int P) {
+__global__ __launch_bounds__(768) void qk_coop_kernel(HeadArgs a, int P, int nt) {
   using S = typename TX::storage;
   using SF = typename TF::storage;
   static_assert(sizeof(S) == 2, "16-bit heads");
@@ -1410,40 +1414,51 @@ __global__ __launch_bounds__(768) void qk_coop_kernel(HeadArgs a, int P) {
     ch_off[i] = (hh - part * HPW) * HROW + (hh == part * HPW + c / CPH ? c % CPH : CPH - 1) * 8;
   }
 
-  float w0[8], w1[8];          // the lane's norm weights
+  // the lane's norm weights of both tensors (the second: the first again
+  // when nt = 1)
+  float wq[2][8], wk[2][8];
   {
-    V8<TW> v0, v1;
-    ld8<TW>(a.weight, c0, v0);
-    ld8<TW>(a.weight, c1, v1);
+    V8<TW> v[4];
+    ld8<TW>(a.weight, c0, v[0]);
+    ld8<TW>(a.weight, c1, v[1]);
+    ld8<TW>(nt > 1 ? a.weight1 : a.weight, c0, v[2]);
+    ld8<TW>(nt > 1 ? a.weight1 : a.weight, c1, v[3]);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) { w0[j] = g8<TW>(v0, j); w1[j] = g8<TW>(v1, j); }
+    for (int j = 0; j < 8; ++j) {
+      wq[0][j] = g8<TW>(v[0], j); wq[1][j] = g8<TW>(v[1], j);
+      wk[0][j] = g8<TW>(v[2], j); wk[1][j] = g8<TW>(v[3], j);
+    }
   }
 
-  // 32-bit token indices (the launcher checks B S < 2^30)
-  const int ntok = (int)(a.B * a.S), ngroups = (ntok + R - 1) / R;
+  // 32-bit row indices (the launcher checks nt B S < 2^30); rows are the
+  // tokens of the first tensor, then those of the second
+  const int ntok = (int)(a.B * a.S), nrows = ntok * nt, ngroups = (nrows + R - 1) / R;
   const int G = gridDim.x;
   if ((int)blockIdx.x >= ngroups) return;   // uniform per block
   const int iters = (ngroups - (int)blockIdx.x + G - 1) / G;
-  // token of this wave in iteration it (past the block's last iteration:
-  // that one again; past the last token: the last token)
-  auto tok_of = [&](int it) {
+  // row of this wave in iteration it (past the block's last iteration: that
+  // one again; past the last row: the last row)
+  auto row_of = [&](int it) {
     it = it < iters ? it : iters - 1;
-    const int t = ((int)blockIdx.x + it * G) * R + sub;
-    return t < ntok ? t : ntok - 1;
+    const int r = ((int)blockIdx.x + it * G) * R + sub;
+    return r < nrows ? r : nrows - 1;
   };
-  struct Tok { int64_t x, o; const uint8_t* t; };
-  auto tok_at = [&](int t) __attribute__((always_inline)) {
+  struct Tok { const S* x; S* o; const uint8_t* t; bool second; };
+  auto tok_at = [&](int r) __attribute__((always_inline)) {
+    const bool second = r >= ntok;
+    const int t = second ? r - ntok : r;
     const int64_t b = (int64_t)a.divS.div((uint64_t)t), s = (int64_t)t - b * a.S;
-    Tok r;
-    r.x = b * a.sb + s * a.ss;
-    r.o = b * a.ob + s * a.os;
-    r.t = static_cast<const uint8_t*>(a.freqs) + (b * a.fb + s * a.fs) * (int64_t)sizeof(SF);
-    return r;
+    Tok k;
+    k.x = static_cast<const S*>(second ? a.x1 : a.x) + b * a.sb + s * a.ss;
+    k.o = static_cast<S*>(second ? a.out1 : a.out) + b * a.ob + s * a.os;
+    k.t = static_cast<const uint8_t*>(a.freqs) + (b * a.fb + s * a.fs) * (int64_t)sizeof(SF);
+    k.second = second;
+    return k;
   };
 
   auto issue = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
-    const Tok tk = tok_at(tok_of(it));
-    const S* xp = static_cast<const S*>(a.x) + tk.x;
+    const Tok tk = tok_at(row_of(it));
+    const S* xp = tk.x;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       bx[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
@@ -1491,11 +1506,12 @@ __global__ __launch_bounds__(768) void qk_coop_kernel(HeadArgs a, int P) {
     v0.v = *reinterpret_cast<const uint4*>(&xs[hslot * HROW + c0]);
     v1.v = *reinterpret_cast<const uint4*>(&xs[hslot * HROW + c1]);
     const SF* tp = reinterpret_cast<const SF*>(trow) + c0 * 4;   // pair c0's entries
+    const Tok tk = tok_at(row_of(it));
     float r0[8], r1[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float y0 = TX::round((g8<TX>(v0, j) * rr) * w0[j]);
-      const float y1 = TX::round((g8<TX>(v1, j) * rr) * w1[j]);
+      const float y0 = TX::round((g8<TX>(v0, j) * rr) * (tk.second ? wk[0][j] : wq[0][j]));
+      const float y1 = TX::round((g8<TX>(v1, j) * rr) * (tk.second ? wk[1][j] : wq[1][j]));
       rotate_pair<TF, F32T>(y0, y1, TF::load(tp[4 * j]), TF::load(tp[4 * j + 1]), TF::load(tp[4 * j + 2]),
                             TF::load(tp[4 * j + 3]), r0[j], r1[j]);
     }
@@ -1505,8 +1521,7 @@ __global__ __launch_bounds__(768) void qk_coop_kernel(HeadArgs a, int P) {
     *reinterpret_cast<uint4*>(&xs[hslot * HROW + c1]) = o1.v;
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
-    const Tok tk = tok_at(tok_of(it));
-    S* op = static_cast<S*>(a.out) + tk.o;
+    S* op = tk.o;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const uint4 v = *reinterpret_cast<const uint4*>(&xs[ch_off[i]]);
@@ -1799,9 +1814,9 @@ int rms_adaln_rows(const void* x, void* out, int dtype, int64_t rows, int64_t D,
 // rotation of 64-, 96- or 128-wide heads, one table row per token, at most 12
 // parts per token); -1 otherwise.
 template <typename TX, typename TW, typename TF>
-static int launch_qk_coop(HeadArgs& a, hipStream_t st) {
+static int launch_qk_coop(HeadArgs& a, hipStream_t st, int nt = 1) {
   const int64_t ntok = a.B * a.S;
-  if (a.rot != a.D || a.fh != 0 || ntok >= (int64_t(1) << 30)) return -1;
+  if (a.rot != a.D || a.fh != 0 || ntok * nt >= (int64_t(1) << 30)) return -1;
   auto go = [&](auto kern, int D) -> int {
     const int lph = D / 16, hpw = 64 / lph;
     const int P = (int)((a.H + hpw - 1) / hpw);
@@ -1811,8 +1826,8 @@ static int launch_qk_coop(HeadArgs& a, hipStream_t st) {
     const size_t rb = (size_t)(D / 2) * 4 * sizeof(typename TF::storage);
     const size_t lds = (size_t)R * P * wslice + 2 * (size_t)R * rb;
     if (lds > LDS_BYTES) return -1;
-    const int64_t grid = std::min<int64_t>((ntok + R - 1) / R, std::max(1, cu_count()));
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * P * R), lds, st, a, P);
+    const int64_t grid = std::min<int64_t>((ntok * nt + R - 1) / R, std::max(1, cu_count()));
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * P * R), lds, st, a, P, nt);
     return check_launch("qk_coop_kernel");
   };
   if (a.D == 64) return go(qk_coop_kernel<TX, TW, TF, 64>, 64);
@@ -1851,6 +1866,58 @@ static int launch_head(HeadArgs& a, int lph, hipStream_t st) {
 #undef XMH3_HT
 #undef XMH3_H
   return fail(XMH3_EUNSUPPORTED, "head-span kernel: head too wide");
+}
+
+// Q and K with one table (the reference's launcher takes both): one launch
+// of the cooperative QK kernel when both tensors have the same strides and
+// it serves the call, else one call per tensor.
+int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
+               const int64_t* xstrides, const int64_t* ostrides, const void* weight,
+               int weight_dtype, const void* freqs, int freqs_dtype, const int64_t* fstrides,
+               int rot_dim, float eps, int norm, int split_half, hipStream_t st);
+int rope_heads_qk(void* q, void* q_out, void* k, void* k_out, int dtype, int64_t B, int64_t S, int64_t H,
+                  int64_t D, const int64_t* qstrides, const int64_t* qostrides, const int64_t* kstrides,
+                  const int64_t* kostrides, const void* q_weight, const void* k_weight, int weight_dtype,
+                  const void* freqs, int freqs_dtype, const int64_t* fstrides, int rot_dim, float eps,
+                  int norm, int split_half, hipStream_t st) {
+  bool same = true;
+  for (int i = 0; i < 3; ++i) same = same && qstrides[i] == kstrides[i] && qostrides[i] == kostrides[i];
+  const int rot = rot_dim ? rot_dim : (int)D;
+  const bool b16 = dtype == DT_BF16 || dtype == DT_F16;
+  if (same && norm && split_half && b16 && rot == D && fstrides[2] == 0 && B * S * H > 0 && q && k && q_out &&
+      k_out && q_weight && k_weight && aligned16(k) && aligned16(k_out) && aligned16(k_weight) &&
+      (weight_dtype == dtype || weight_dtype == DT_F32)) {
+    // the first tensor's checks, and the arguments, come from rope_heads
+    // with a launch-free probe: validate by building the same HeadArgs
+    XMH3_REQUIRE(D > 0 && rot % 16 == 0 && D <= 512, "rope: bad head_dim");
+    for (int i = 0; i < 3; ++i)
+      XMH3_REQUIRE(qstrides[i] % 8 == 0 && qostrides[i] % 8 == 0 && fstrides[i] % 8 == 0,
+                   "rope: strides must be multiples of 8 elements");
+    XMH3_REQUIRE(aligned16(q) && aligned16(q_out) && aligned16(freqs) && aligned16(q_weight),
+                 "rope: pointers must be 16-byte aligned");
+    HeadArgs a{};
+    a.x = q; a.out = q_out; a.B = B; a.S = S; a.H = H; a.D = D;
+    a.sb = qstrides[0]; a.ss = qstrides[1]; a.sh = qstrides[2];
+    a.ob = qostrides[0]; a.os = qostrides[1]; a.oh = qostrides[2];
+    a.weight = q_weight; a.freqs = freqs; a.fb = fstrides[0]; a.fs = fstrides[1]; a.fh = fstrides[2];
+    a.divS = FastDivU64::make((uint64_t)S); a.divH = FastDivU64::make((uint64_t)H);
+    a.rot = rot; a.eps = eps;
+    a.x1 = k; a.out1 = k_out; a.weight1 = k_weight;
+    int rc = -1;
+#define XMH3_QK(TX, TF)                                                                      \
+    rc = weight_dtype == DT_F32 ? launch_qk_coop<TX, F32T, TF>(a, st, 2) : launch_qk_coop<TX, TX, TF>(a, st, 2);
+    if (dtype == DT_BF16 && freqs_dtype == DT_F32) { XMH3_QK(BF16T, F32T) }
+    else if (dtype == DT_BF16 && freqs_dtype == DT_BF16) { XMH3_QK(BF16T, BF16T) }
+    else if (dtype == DT_F16 && freqs_dtype == DT_F32) { XMH3_QK(F16T, F32T) }
+    else if (dtype == DT_F16 && freqs_dtype == DT_F16) { XMH3_QK(F16T, F16T) }
+#undef XMH3_QK
+    if (rc != -1) return rc;
+  }
+  const int rc = rope_heads(q, q_out, dtype, B, S, H, D, qstrides, qostrides, q_weight, weight_dtype, freqs,
+                            freqs_dtype, fstrides, rot_dim, eps, norm, split_half, st);
+  if (rc != XMH3_OK) return rc;
+  return rope_heads(k, k_out, dtype, B, S, H, D, kstrides, kostrides, k_weight, weight_dtype, freqs, freqs_dtype,
+                    fstrides, rot_dim, eps, norm, split_half, st);
 }
 
 int rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t D,
@@ -1959,6 +2026,14 @@ extern "C" void launch_rms_rope_kernel(
     return reject("launch_rms_rope_kernel: table dimensions must be 1 or match the input");
   const int64_t fst[3] = {freqs_batch == 1 ? 0 : f_s0, freqs_dim1 == 1 ? 0 : f_s1, freqs_dim2 == 1 ? 0 : f_s2};
   const int norm = q_scale != nullptr;
+  if (has_k && norm) {
+    const int64_t xs[3] = {q_s0, q_s1, q_s2}, os[3] = {qo_s0, qo_s1, qo_s2};
+    const int64_t ks[3] = {k_s0, k_s1, k_s2}, kos[3] = {ko_s0, ko_s1, ko_s2};
+    rope_heads_qk(const_cast<void*>(q), q_out, const_cast<void*>(k), k_out, input_dtype_code, batch, dim1, dim2,
+                  head_dim, xs, os, ks, kos, q_scale, k_scale ? k_scale : q_scale, scale_dtype_code, freqs,
+                  freqs_dtype_code, fst, (int)rot_dim, epsilon, norm, split_half, stream);
+    return;
+  }
   {
     const int64_t xs[3] = {q_s0, q_s1, q_s2}, os[3] = {qo_s0, qo_s1, qo_s2};
     if (rope_heads(const_cast<void*>(q), q_out, input_dtype_code, batch, dim1, dim2, head_dim, xs, os, q_scale,
@@ -1983,6 +2058,18 @@ extern "C" int xmh3_rope_split_half(void* x, void* out, int dtype, int64_t B, in
   return xmh3::rope_heads(x, out, dtype, B, S, H, head_dim, x_strides, out_strides, norm_weight,
                           weight_dtype, freqs, freqs_dtype, freqs_strides, rot_dim, eps, norm, 1,
                           stream);
+}
+
+extern "C" int xmh3_rope_heads_qk(void* q, void* q_out, void* k, void* k_out, int dtype, int64_t B, int64_t S,
+                                  int64_t H, int64_t head_dim, const int64_t* q_strides,
+                                  const int64_t* q_out_strides, const int64_t* k_strides,
+                                  const int64_t* k_out_strides, const void* q_weight, const void* k_weight,
+                                  int weight_dtype, const void* freqs, int freqs_dtype,
+                                  const int64_t* freqs_strides, int rot_dim, float eps, int norm, int split_half,
+                                  hipStream_t stream) {
+  return xmh3::rope_heads_qk(q, q_out, k, k_out, dtype, B, S, H, head_dim, q_strides, q_out_strides, k_strides,
+                             k_out_strides, q_weight, k_weight, weight_dtype, freqs, freqs_dtype, freqs_strides,
+                             rot_dim, eps, norm, split_half, stream);
 }
 
 extern "C" int xmh3_rope_heads(void* x, void* out, int dtype, int64_t B, int64_t S, int64_t H, int64_t head_dim,
