@@ -605,6 +605,8 @@ def test_rope_table_paths(pkg, dev, heads, per_head_table):
     (389, 40, 128, torch.float32, torch.bfloat16, torch.bfloat16, True),
     (211, 30, 96, torch.float16, torch.float16, torch.float16, False),
     (5, 7, 96, torch.float32, torch.bfloat16, torch.bfloat16, True),        # fewer heads than a part holds
+    (1, 1, 64, torch.float32, torch.bfloat16, torch.bfloat16, False),       # one token, one head
+    (257, 16, 64, torch.bfloat16, torch.bfloat16, torch.bfloat16, True),    # exactly one part per token
 ])
 def test_qk_rope_pair_launch(pkg, dev, S, H, D, tdtype, wdtype, dtype, inplace):
     """Q and K through one call of the pair entry (one launch of the
@@ -627,6 +629,26 @@ def test_qk_rope_pair_launch(pkg, dev, S, H, D, tdtype, wdtype, dtype, inplace):
     torch.cuda.synchronize()
     assert same(oq, cpu_ref.rms_rope_split_half1(xq, tab, qw, 1e-5, 0), "q")
     assert same(ok, cpu_ref.rms_rope_split_half1(xk, tab, kw, 1e-5, 0), "k")
+
+
+def test_qk_rope_pair_packed_qkv_full_rotation(pkg, dev):
+    """Full 128-wide rotation in place on the Q and K views of a packed QKV
+    tensor (token stride 3·H·D, shared by Q and K): the pair launch with a
+    token stride other than H·D; V is untouched."""
+    say("rms_rope_split_half_ full rotation on packed qkv views")
+    g = torch.Generator().manual_seed(31)
+    S, H, D = 1031, 12, 128
+    qkv = torch.randn(1, S, 3, H, D, generator=g).to(torch.bfloat16)
+    tab = _angle_table((1, S, 1), D // 2, 32, torch.float32)
+    qw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    kw = (torch.rand(D, generator=g) + 0.5).to(torch.bfloat16)
+    dq = qkv.to(dev)
+    pkg.rms_rope_split_half_(dq[:, :, 0], dq[:, :, 1], tab.to(dev), qw.to(dev), kw.to(dev), 1e-5, 0)
+    torch.cuda.synchronize()
+    out = dq.cpu()
+    assert same(out[:, :, 0], cpu_ref.rms_rope_split_half1(qkv[:, :, 0], tab, qw, 1e-5, 0), "q")
+    assert same(out[:, :, 1], cpu_ref.rms_rope_split_half1(qkv[:, :, 1], tab, kw, 1e-5, 0), "k")
+    assert torch.equal(out[:, :, 2], qkv[:, :, 2])    # v untouched
 
 
 def test_h3_qknorm_rope_partial_inplace(pkg, dev):
@@ -720,6 +742,10 @@ def test_rms_adaln(pkg, dev, mod_dtype):
     (700, 1056, ((0, 50, 0), (50, 600, 1), (600, 700, 2))),
     (500, 2560, ((0, 1, 0), (1, 499, 1), (499, 500, 2))),
     (200, 11776, ((0, 13, 0), (13, 100, 1), (100, 200, 2))),
+    # tiny rows: one 32-element part (no full chunk), one row, two rows
+    (5, 32, ((0, 1, 0), (1, 2, 1), (2, 5, 2))),
+    (1, 1024, ((0, 1, 1),)),
+    (2, 5376, ((0, 1, 2), (1, 2, 0))),
 ])
 def test_h3_segmented_rms_adaln(pkg, dev, rows, width, segs):
     say(f"h3 segmented rms_adaln rows={rows} width={width}")
@@ -735,6 +761,26 @@ def test_h3_segmented_rms_adaln(pkg, dev, rows, width, segs):
     want = cpu_ref.rms_adaln_segmented(x, w, sh, sc, segs, eps=1e-5)
     close(out, want, "segmented rms_adaln")
     assert same(out, want, "segmented rms_adaln")
+
+
+@pytest.mark.parametrize("rows,width", [(777, 5376), (3, 2048)])
+def test_rms_adaln_rows_without_norm_weight(pkg, dev, rows, width):
+    """The row-map form with no norm weight (plain rms_norm before the
+    modulation), against the oracle bit for bit."""
+    say(f"rms_adaln rows without weight rows={rows} width={width}")
+    from x_minimaxh3_amd import backend
+
+    g = torch.Generator().manual_seed(rows + width)
+    x = torch.randn(rows, width, generator=g).to(torch.bfloat16)
+    sc = (torch.randn(2, width, generator=g) * 0.1).to(torch.bfloat16)
+    sh = (torch.randn(2, width, generator=g) * 0.1).to(torch.bfloat16)
+    cut = rows // 2
+    rm = torch.cat((torch.zeros(cut, dtype=torch.int32), torch.ones(rows - cut, dtype=torch.int32)))
+    out = backend.rms_adaln_rows(x.to(dev), None, sc.to(dev), sh.to(dev), rm.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    segs = ((0, cut, 0), (cut, rows, 1)) if cut else ((0, rows, 1),)
+    want = cpu_ref.rms_adaln_segmented(x, None, sh, sc, segs, eps=1e-6)
+    assert same(out, want, "rms_adaln without weight")
 
 
 def test_h3_segmented_rms_adaln_many_iterations(pkg, dev):
