@@ -1,7 +1,15 @@
 // Memory-bound normalisation / rotary kernels for gfx950.
 //
+// Cooperative family (the measured paths): a row split over the waves of a
+// block, one block per CU streaming row groups with two groups of loads in
+// flight, the reference-order reduction assembled through LDS:
+//   * norm_rope_coop_kernel : norm_rope of Q and K rows, width % 1024 == 0
+//   * adaln_coop_kernel     : rms_adaln of bf16 rows with bf16 modulation
+//   * qk_coop_kernel        : per-head rms_norm + full split-half rotation of
+//                             64/96/128-wide heads, Q and K in one launch
 // Row-span family (one wave64 per token row, the row held in VGPRs, 16-byte
-// loads and stores, wave reduction of the sum of squares, no LDS):
+// loads and stores, wave reduction of the sum of squares, no LDS), for the
+// widths, dtypes and modulation forms the cooperative kernels do not take:
 //   * norm_rope  : out = rope_split_half(rms_adaln(x, scale, shift, eps), freqs)
 //                  for Q and K of one token in the same wave (the table row is
 //                  read once for both); RMS over the full row, rotation per
@@ -11,7 +19,8 @@
 //                  modulation row r = row_map[token] or token / group
 //                  (CK/backends/eager/adaln.py:17-20,
 //                   h3serve/native_engine/model/kernels.py:7623-7634)
-// Head-span family (a power-of-two group of lanes per (token, head)):
+// Head-span family (a power-of-two group of lanes per (token, head)), for
+// the rotary calls the cooperative QK kernel does not take:
 //   * rms_rope_split_half : per-head rms_norm with weight, split-half rotation
 //                  of the first rot_dim dims, tail norm-only, in place on
 //                  strided [B,S,H,D] (CK/backends/eager/rope.py:67-92,178-189)
