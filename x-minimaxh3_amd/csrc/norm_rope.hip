@@ -1486,22 +1486,26 @@ __global__ __launch_bounds__(768) void qk_coop_kernel(HeadArgs a, int P, int nt)
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the staging stores are done
     __builtin_amdgcn_wave_barrier();
+    // job pairs (head, v), (head, v + 1), v even: each 32-bit read holds
+    // the elements of chains v + 8 g and v + 1 + 8 g; NJOB / 2 <= 64 lanes
+    static_assert(NJOB / 2 <= 64, "one round of job pairs");
+    if (lane < NJOB / 2) {
+      const S* hr = xs + (lane >> 2) * HROW;
+      const int v = (lane & 3) * 2;
+      float r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
-    for (int q = 0; q < (NJOB + 63) / 64; ++q) {
-      const int j = lane + 64 * q;
-      if (j < NJOB) {
-        const S* hr = xs + (j >> 3) * HROW;
-        const int v = j & 7;
-        float r = 0.0f;
+      for (int g = 0; g < 4; ++g) {
+        float c0 = 0.0f, c1 = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float c = 0.0f;
-#pragma unroll
-          for (int i = 0; i < STEPS; ++i) c = add_sq<TX>(c, TX::load(hr[i * 32 + v + 8 * g]));
-          r = g ? r + c : c;
+        for (int i = 0; i < STEPS; ++i) {
+          const uint32_t w2 = *reinterpret_cast<const uint32_t*>(hr + i * 32 + v + 8 * g);
+          c0 = add_sq<TX>(c0, TX::load(w2 & 0xffffu));
+          c1 = add_sq<TX>(c1, TX::load(w2 >> 16));
         }
-        rs[j] = r;
+        r0 = g ? r0 + c0 : c0;
+        r1 = g ? r1 + c1 : c1;
       }
+      *reinterpret_cast<float2*>(rs + (lane >> 2) * 8 + v) = make_float2(r0, r1);
     }
     // publish the job results and the table slices (LDS only: the
     // prefetched rows stay in flight)
