@@ -501,6 +501,23 @@ def test_norm_rope_720p(pkg, dev):
         assert same(got, want, f"norm_rope {name}")   # reference reduction order -> bit exact
 
 
+def test_norm_rope_720p_in_place(pkg, dev):
+    """The cooperative norm-rope in place at 720p (about 66 row groups per
+    block, both parities of the last iteration's redo, the last partial
+    group): equal to the out-of-place result bit for bit."""
+    say("norm_rope 25200x5120 in place")
+    from x_minimaxh3_amd import backend, workloads
+
+    nr = workloads.norm_rope_inputs(grid=(7, 45, 80))
+    qd, kd = nr["q"].to(dev), nr["k"].to(dev)
+    scd, shd, fd = nr["scale"].to(dev), nr["shift"].to(dev), nr["freqs"].to(dev)
+    qo, ko = backend.norm_rope(qd, kd, scd, shd, fd, nr["eps"], 128)
+    qi, ki = qd.clone(), kd.clone()
+    backend.norm_rope(qi, ki, scd, shd, fd, nr["eps"], 128, inplace=True)
+    torch.cuda.synchronize()
+    assert torch.equal(qi, qo) and torch.equal(ki, ko)
+
+
 @pytest.mark.parametrize("d,m,with_k,tab_dtype,bcast,dtype", [
     (5120, 37, True, torch.float32, False, torch.bfloat16),    # cooperative kernel, fewer tokens than blocks
     (5120, 1000, False, torch.float32, False, torch.bfloat16),  # Q only
