@@ -56,7 +56,7 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 TRAFFIC_BYTES = {
     "fc1_gemm": (1699000.0 * 2 + 680400.0) * 1024,
     "fc2_gemm": (1481000.0 * 2 + 252000.0) * 1024,
-    "norm_rope": (281200.0 * 2 + 508800.0) * 1024,
+    "norm_rope": (281245.0 * 2 + 506827.0) * 1024,
 }
 
 

@@ -455,19 +455,20 @@ struct SwizzledRowIdx {
 // of 512 positions: chain L adds the 16 squares at 512 j + 32 u + L from zero
 // (u = 0..15) and folds the chunk sum into its cascade. A part holds chunks
 // 2 p and 2 p + 1 whole, so each wave computes its 2 x 32 chunk sums from its
-// staged part, the block shares them in LDS, and after one barrier every
-// wave folds the row's 2P chunk sums in order and combines the chains as
-// ref_order_sumsq does: bit-identical rrms. D % 1024 == 0 leaves no partial
-// chunk and no leftover vector.
+// staged part, the block shares them in LDS, and after one barrier one wave
+// of the row folds the row's 2P chunk sums in order and combines the chains
+// as ref_order_sumsq does (bit-identical rrms) and publishes the rrms, which
+// the row's waves use after the next iteration's barrier. D % 1024 == 0
+// leaves no partial chunk and no leftover vector.
 //
 // Two rows are prefetched in registers (2 items of 16 bytes per lane per row,
-// plus the row's table row, 16 bytes per lane). Chunk sums and the table row
-// live in two parity slots, so one barrier per row suffices: a slot is
-// rewritten two rows later, after every wave has passed the barrier that
+// plus the row's table row, 16 bytes per lane). Staging, chunk sums and rrms
+// live in two parity slots and table rows in three, so one barrier per row
+// suffices: a slot is rewritten after every wave has passed the barrier that
 // follows its last read. The barrier waits for LDS only (__syncthreads would
 // also wait for the prefetched loads).
-// LDS: 8 D (modulation, ADALN) + 2 KB per wave (staging) + 2 * R * 2P * 32
-// floats (chunk sums) + 2 R table rows.
+// LDS: 8 D (modulation, ADALN) + 4 KB per wave (staging) + 2 * R * 2P * 32
+// floats (chunk sums) + 3 R table rows + 2 R floats (rrms).
 // ---------------------------------------------------------------------------
 template <typename TX, typename TF, bool ADALN, int P>
 __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt) {
@@ -489,9 +490,10 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
   f32x4* lt = reinterpret_cast<f32x4*>(dyn_lds);
   f32x4* ls = lt + D / 4;
   uint8_t* p0 = dyn_lds + (ADALN ? 8 * D : 0);
-  S* stage = reinterpret_cast<S*>(p0 + w * 2048);
-  float* sums = reinterpret_cast<float*>(p0 + R * P * 2048);           // [2][R][NCH][32]
-  u32x4* tabs = reinterpret_cast<u32x4*>(sums + 2 * R * NCH * 32);     // [2][R][TAB_CHUNKS]
+  S* stage = reinterpret_cast<S*>(p0 + w * 4096);                     // [2][1024] per wave
+  float* sums = reinterpret_cast<float*>(p0 + R * P * 4096);           // [2][R][NCH][32]
+  u32x4* tabs = reinterpret_cast<u32x4*>(sums + 2 * R * NCH * 32);     // [3][R][TAB_CHUNKS]
+  float* rrs = reinterpret_cast<float*>(tabs + 3 * R * TAB_CHUNKS);    // [2][R]
 
   if constexpr (ADALN) {
     // t = round_TX(1 + scale), sh = shift, as fp32, lane-major: float4
@@ -551,13 +553,31 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
     bt = *reinterpret_cast<const u32x4*>(tb + tab_lane * EPC);
   };
 
-  int par = 0;
-  auto process = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
-    const int row = row_of(it);
+  // Iteration it: front(it) stages row_of(it), prefetches iteration it + 2,
+  // publishes its chunk sums and, after the barrier, one wave of the row
+  // (part rpart) folds them into the row's rrms; back(it - 1) then runs the
+  // element pass of the previous iteration's row, whose rrms that wave
+  // published before this barrier. Only one wave per row folds, combines and
+  // divides (every wave doing it cost 3-5 % of the kernel), with no extra
+  // barrier: the element pass trails the reduction by one iteration. Slots:
+  // staging and rrms in two (parity), table rows in three (written before the
+  // barrier of iteration it, read after that of it + 1, rewritten before that
+  // of it + 3).
+  //
+  // The folding wave is the row's wave w with w % 4 == 3 where the row has
+  // one: waves are dealt to the CU's four SIMDs in turn, and a block of 15
+  // waves (P = 5, R = 3) leaves SIMD 3 one wave short, so the extra work goes
+  // there (folding on part 0 put it on SIMDs 0-2 and measured 2-3 % slower).
+  // The choice only moves work; any wave of the row gives the same bits.
+  int par = 0, tsl = 0;
+  const int rp0 = ((3 - sub * P) % 4 + 4) % 4;
+  const int rpart = rp0 < P ? rp0 : 0;
+  auto front = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
+    S* sg = stage + par * 1024;
     const int slot = par * R + sub;
-    *reinterpret_cast<u32x4*>(stage + sl0) = bx[0];
-    *reinterpret_cast<u32x4*>(stage + sl1) = bx[1];
-    if (part == 0 && lane < TAB_CHUNKS) tabs[slot * TAB_CHUNKS + tab_slot] = bt;
+    *reinterpret_cast<u32x4*>(sg + sl0) = bx[0];
+    *reinterpret_cast<u32x4*>(sg + sl1) = bx[1];
+    if (part == 0 && lane < TAB_CHUNKS) tabs[(tsl * R + sub) * TAB_CHUNKS + tab_slot] = bt;
     __builtin_amdgcn_sched_barrier(0);
     issue(it + 2, bx, bt);
     __builtin_amdgcn_sched_barrier(0);
@@ -569,7 +589,7 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
       float c = 0.0f;
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
-        const float v = TX::load(stage[SwizzledRowIdx{}(h * 512 + u * 32 + L)]);
+        const float v = TX::load(sg[SwizzledRowIdx{}(h * 512 + u * 32 + L)]);
         c = add_sq<TX>(c, v);
       }
       sums[(slot * NCH + 2 * part + h) * 32 + L] = c;
@@ -577,8 +597,7 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
     // publish the chunk sums (and wave 0's table row) to the block
     __builtin_amdgcn_s_waitcnt(0xc07f);
     asm volatile("s_barrier" ::: "memory");
-    float rr;
-    {
+    if (part == rpart) {
       // the reference order: fold the row's chunk sums, then the chains
       const int L = lane & 31;
       const float* cs = sums + slot * NCH * 32 + L;
@@ -604,15 +623,22 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
       float fin = 0.0f;
 #pragma unroll
       for (int v = 0; v < 8; ++v) fin = fin + __shfl(pv, v, 64);
-      rr = 1.0f / sqrtf(fin / (float)D + a.eps);
+      if (lane == 0) rrs[slot] = 1.0f / sqrtf(fin / (float)D + a.eps);
     }
+  };
+  // element pass of row_of(it), staged by the previous front()
+  auto back = [&](int it) __attribute__((always_inline)) {
+    const int row = row_of(it);
+    const int pp = par ^ 1, ts = tsl == 0 ? 2 : tsl - 1;
+    const S* sg = stage + pp * 1024;
+    const float rr = rrs[pp * R + sub];
     // this lane's 8 pairs (it8 .. it8 + 7) of the token's table row
     Tab8<TF> tab;
     {
       SF el[CPG * EPC];
 #pragma unroll
       for (int j = 0; j < CPG; ++j) {
-        const u32x4 v = tabs[slot * TAB_CHUNKS + j * IPH + (lane % IPH)];
+        const u32x4 v = tabs[(ts * R + sub) * TAB_CHUNKS + j * IPH + (lane % IPH)];
 #pragma unroll
         for (int e = 0; e < EPC; ++e) {
           if constexpr (sizeof(SF) == 4) el[j * EPC + e] = __uint_as_float(v[e]);
@@ -620,15 +646,15 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
         }
       }
 #pragma unroll
-      for (int pp = 0; pp < 8; ++pp)
+      for (int pp2 = 0; pp2 < 8; ++pp2)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tab.f[pp][e] = TF::load(el[pp * 4 + e]);
+        for (int e = 0; e < 4; ++e) tab.f[pp2][e] = TF::load(el[pp2 * 4 + e]);
     }
     float y[2][8];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       V8<TX> xv;
-      xv.v = *reinterpret_cast<const uint4*>(stage + (h ? sl1 : sl0));
+      xv.v = *reinterpret_cast<const uint4*>(sg + (h ? sl1 : sl0));
       float t8[8], sh8[8];
       if constexpr (ADALN) {
         const int i0 = ((part * 2 + h) * 2) * 64 + lane;
@@ -673,31 +699,49 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
       __builtin_nontemporal_store(u32x4{w0[0], w0[1], w0[2], w0[3]}, reinterpret_cast<u32x4*>(ob));
       __builtin_nontemporal_store(u32x4{w1[0], w1[1], w1[2], w1[3]}, reinterpret_cast<u32x4*>(ob + HD / 2));
     }
-    // the next row's staging overwrites this wave's slice
+  };
+  auto next = [&]() __attribute__((always_inline)) {
+    // LDS work of this iteration done before the slots turn over
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
     par ^= 1;
+    tsl = tsl == 2 ? 0 : tsl + 1;
   };
 
   // Two row groups in flight, in two register buffers taken in turn. The
-  // first iteration is peeled off the loop and the loop body is two whole
-  // iterations with its only exit at the bottom: the loop head is then
-  // reached only with the other buffer's loads, one prefetch and its stores
-  // outstanding, as on the back edge, so the compiler's waits there leave the
-  // prefetched group in flight (a loop with an exit between its two halves
-  // gives the head a path with fewer operations outstanding, and the waits
-  // then drain the prefetch). An odd count ends with one extra iteration
-  // that redoes the block's last one: its loads were issued before that
-  // iteration's stores, so it stores identical bytes, also in place.
+  // first two iterations are peeled off the loop (the first has no element
+  // pass) and the loop body is two whole iterations with its only exit at the
+  // bottom: the loop head is then reached with the other buffer's loads
+  // outstanding after the buffer it consumes, so the compiler's waits there
+  // leave the prefetched group in flight (a path with fewer operations
+  // outstanding makes those waits drain the prefetch). The peeled path has
+  // one group of stores fewer than the back edge, so on the back edge the
+  // head also waits for the stores of two iterations back, older than the
+  // prefetch; peeling a third iteration removes that wait and measured 1-2 %
+  // slower. A count that leaves the last pair half full ends with one extra
+  // iteration that redoes the block's last one: its loads were issued before
+  // that row's stores, so it stores identical bytes, also in place. A last
+  // barrier publishes the last row's rrms for its element pass.
   u32x4 x0[2], x1[2], t0, t1;
   issue(0, x0, t0);
   issue(1, x1, t1);
   __builtin_amdgcn_sched_barrier(0);
-  process(0, x0, t0);
-  for (int it = 1; it < iters; it += 2) {
-    process(it, x1, t1);
-    process(it + 1, x0, t0);
+  front(0, x0, t0);
+  next();
+  front(1, x1, t1);
+  back(0);
+  next();
+  for (int it = 2; it < iters; it += 2) {
+    front(it, x0, t0);
+    back(it - 1);
+    next();
+    front(it + 1, x1, t1);
+    back(it);
+    next();
   }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  asm volatile("s_barrier" ::: "memory");
+  back(iters - 1);
   __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): no load lands after the wave ends
 }
 
@@ -1705,8 +1749,8 @@ template <typename TX, typename TF, bool ADALN, int P>
 static int launch_coop_p(RowArgs& a, int nt, hipStream_t st) {
   if (a.rows * nt >= (int64_t(1) << 30)) return -1;   // 32-bit row indices
   const int R = std::max(1, std::min(XMH3_COOP_ROWS, 16 / P));
-  const size_t lds = (ADALN ? 8 * (size_t)a.D : 0) + (size_t)R * P * 2048 + (size_t)2 * R * 2 * P * 32 * 4 +
-                     2 * (size_t)R * 64 * 4 * sizeof(typename TF::storage);
+  const size_t lds = (ADALN ? 8 * (size_t)a.D : 0) + (size_t)R * P * 4096 + (size_t)2 * R * 2 * P * 32 * 4 +
+                     3 * (size_t)R * 64 * 4 * sizeof(typename TF::storage) + 2 * (size_t)R * 4;
   if (lds > LDS_BYTES) return -1;
   auto kern = norm_rope_coop_kernel<TX, TF, ADALN, P>;
   static bool attr_set = false;
