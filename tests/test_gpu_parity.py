@@ -501,14 +501,16 @@ def test_norm_rope_720p(pkg, dev):
         assert same(got, want, f"norm_rope {name}")   # reference reduction order -> bit exact
 
 
-def test_norm_rope_720p_in_place(pkg, dev):
-    """The cooperative norm-rope in place at 720p (about 66 row groups per
-    block, both parities of the last iteration's redo, the last partial
-    group): equal to the out-of-place result bit for bit."""
-    say("norm_rope 25200x5120 in place")
+@pytest.mark.parametrize("grid", [(7, 45, 80), (1, 20, 50), (1, 1, 37)])
+def test_norm_rope_in_place(pkg, dev, grid):
+    """The cooperative norm-rope in place: at 720p 65 or 66 row groups per
+    block (with and without the redo of a block's last iteration) and the
+    last partial group; 1000 tokens give 2 or 3 row groups per block, 37
+    tokens one. Equal to the out-of-place result bit for bit."""
+    say(f"norm_rope grid {grid} in place")
     from x_minimaxh3_amd import backend, workloads
 
-    nr = workloads.norm_rope_inputs(grid=(7, 45, 80))
+    nr = workloads.norm_rope_inputs(grid=grid)
     qd, kd = nr["q"].to(dev), nr["k"].to(dev)
     scd, shd, fd = nr["scale"].to(dev), nr["shift"].to(dev), nr["freqs"].to(dev)
     qo, ko = backend.norm_rope(qd, kd, scd, shd, fd, nr["eps"], 128)
@@ -520,6 +522,8 @@ def test_norm_rope_720p_in_place(pkg, dev):
 
 @pytest.mark.parametrize("d,m,with_k,tab_dtype,bcast,dtype", [
     (5120, 37, True, torch.float32, False, torch.bfloat16),    # cooperative kernel, fewer tokens than blocks
+    (5120, 1000, True, torch.float32, False, torch.bfloat16),   # 2 or 3 row groups per block
+    (2048, 1900, True, torch.float32, False, torch.bfloat16),   # 3 or 4 row groups per block
     (5120, 1000, False, torch.float32, False, torch.bfloat16),  # Q only
     (3072, 1000, True, torch.bfloat16, False, torch.bfloat16),  # bf16 table
     (1024, 4099, True, torch.float32, True, torch.bfloat16),    # one broadcast table row
