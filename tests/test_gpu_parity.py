@@ -61,9 +61,9 @@ def outlier_acts(m, k, seed=0, n_out=8, dtype=torch.bfloat16):
 
 @pytest.mark.parametrize("m,k,dtype", [
     (25200, 5120, torch.bfloat16),   # fc1 input of the 720p MLP
-    (999, 13824, torch.bfloat16),    # fc2 width, ragged rows (two waves per row)
-    (7, 9000, torch.float16),        # two waves per row, odd rows, uneven halves
-    (3, 8704, torch.float32),        # two waves per row, fp32 rows
+    (999, 13824, torch.bfloat16),    # fc2 width (four waves per row)
+    (7, 9000, torch.float16),        # four waves per row, uneven quarters
+    (3, 8704, torch.float32),        # four waves per row, fp32 rows
     (37, 1536, torch.float16),
     (33, 520, torch.float32),
     (7, 20000, torch.bfloat16),      # wider than the register path
@@ -126,7 +126,7 @@ def test_quantize_with_gelu_input_act(pkg, dev):
     say("quantize gelu input act")
     from x_minimaxh3_amd import backend
 
-    h = outlier_acts(513, 13824, seed=3) * 0.5   # odd rows: the last block's second row is empty
+    h = outlier_acts(513, 13824, seed=3) * 0.5   # fc2 width: four waves per row, GELU in registers
     q, s = backend._quantize(h.to(dev), 1)
     torch.cuda.synchronize()
     g = cpu_ref.gelu_tanh(h)

@@ -182,32 +182,29 @@ __global__ __launch_bounds__(256) void quant_rows_reg_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// register-resident path for wide rows: WPR waves per row, wave w taking the
-// 512-element steps w, w + WPR, w + 2 WPR, ... (NL each), so 1/WPR of the
-// row's registers per wave and more waves per SIMD to hide the loads; the
-// partial maxima meet in LDS. Same per-element operations as the one-wave
-// path, and max is order-free, so the codes and scale are identical.
+// register-resident path for wide rows: a block of WPR = 4 waves per row
+// (one row per block), wave w taking the 512-element steps w, w + 4,
+// w + 8, ... (NL each), so a quarter of the row's registers per wave and more
+// waves per SIMD to hide the loads; the partial maxima meet in LDS. Same
+// per-element operations as the one-wave path, and max is order-free, so the
+// codes and scale are identical.
 // ---------------------------------------------------------------------------
-#ifndef XMH3_QWPR
-#define XMH3_QWPR 4
-#endif
 template <typename T, int ACT, int NL, int WPR>
 __global__ __launch_bounds__(256) void quant_rows_reg2_kernel(
     const typename T::storage* __restrict__ x, int64_t ldx, int64_t M, int64_t K,
     int8_t* __restrict__ q, int64_t ldq, float* __restrict__ scale,
     uint32_t* __restrict__ zero_rows) {
-  static_assert(WPR == 2 || WPR == 4, "2 or 4 waves per row");
+  static_assert(WPR == 4, "a block of 4 waves per row");
   __shared__ float part_max[4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = wave % WPR;
-  const int64_t row = (int64_t)blockIdx.x * (4 / WPR) + wave / WPR;
-  const bool row_ok = row < M;
-  const typename T::storage* xr = x + (row_ok ? row : 0) * ldx;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = wave;
+  const int64_t row = blockIdx.x;   // the grid has M blocks
+  const typename T::storage* xr = x + row * ldx;
   Pack8<T> buf[NL];
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < NL; ++i) {
     const int64_t col = ((int64_t)(WPR * i + half) * 64 + lane) * 8;
-    if (row_ok && col < K) {
+    if (col < K) {
       load8<T>(xr + col, buf[i]);
       if constexpr (ACT == ACT_GELU_TANH && sizeof(typename T::storage) == 2) {
 #pragma unroll
@@ -232,12 +229,10 @@ __global__ __launch_bounds__(256) void quant_rows_reg2_kernel(
   amax = wave_max(amax);
   if (lane == 0) part_max[wave] = amax;
   __syncthreads();
-  if (!row_ok) return;
   {
-    const int w0 = wave - half;
-    float m = part_max[w0];
+    float m = part_max[0];
 #pragma unroll
-    for (int w = 1; w < WPR; ++w) m = fmaxf(m, part_max[w0 + w]);
+    for (int w = 1; w < WPR; ++w) m = fmaxf(m, part_max[w]);
     amax = T::round(m);
   }
   const float s = row_scale(amax);
@@ -387,8 +382,8 @@ static int launch_quant_T(const void* x, int64_t ldx, int64_t M, int64_t K, int8
                       ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
   const int64_t steps = (K + 511) / 512;
   if (vec_ok && steps > 16 && steps <= 32 && M <= (1LL << 24)) {
-    constexpr int W = XMH3_QWPR, RPB = 4 / W;   // waves per row, rows per block
-    dim3 grid((unsigned)((M + RPB - 1) / RPB));
+    constexpr int W = 4;   // waves per row, one row per block
+    dim3 grid((unsigned)M);
 #define XMH3_Q2(NLV)                                                                                    \
   if ((steps + W - 1) / W <= NLV) {                                                                     \
     hipLaunchKernelGGL((quant_rows_reg2_kernel<T, ACT, NLV, W>), grid, dim3(256), 0, st, xs, ldx, M, K, \
