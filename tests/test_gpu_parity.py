@@ -577,6 +577,34 @@ def test_norm_rope_per_sample_modulation(pkg, dev):
             assert same(got[b], want, f"norm_rope sample {b}")
 
 
+
+@pytest.mark.parametrize("d,m,with_k", [(5120, 1000, True), (3072, 777, True), (2048, 300, False)])
+def test_norm_rope_abi_without_modulation(pkg, dev, d, m, with_k):
+    """xmh3_norm_rope with scale = shift = NULL (RMSNorm + rotation, the
+    cooperative kernel without AdaLN), through the C ABI: equal to the
+    oracle's norm-rope with zero scale and shift (1 + 0 and + 0 are exact)."""
+    say(f"norm_rope C ABI without modulation d={d} m={m} k={with_k}")
+    from x_minimaxh3_amd import _lib
+
+    g = torch.Generator().manual_seed(d + 3 * m)
+    q = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    k = torch.randn(m, d, generator=g).to(torch.bfloat16)
+    ang = torch.rand(1, m, 1, 64, generator=g) * 40
+    c, s_ = torch.cos(ang), torch.sin(ang)
+    tab = torch.stack((c, -s_, s_, c), -1).reshape(1, m, 1, 64, 2, 2)
+    qd, kd, td = q.to(dev), k.to(dev), tab.to(dev).contiguous()
+    qo = torch.empty_like(qd)
+    ko = torch.empty_like(kd) if with_k else None
+    st = _lib.stream_of(qd)
+    _lib.call("xmh3_norm_rope", qd.data_ptr(), qo.data_ptr(), kd.data_ptr() if with_k else None,
+              ko.data_ptr() if with_k else None, 2, m, d, d, d, None, None, 2, 0, m,
+              td.data_ptr(), 0, 256, 128, 1e-6, st)
+    torch.cuda.synchronize()
+    zero = torch.zeros(1, d, dtype=torch.bfloat16)
+    for got, x in ((qo, q), (ko, k)) if with_k else ((qo, q),):
+        want = cpu_ref.norm_rope(x, zero, zero, tab, 128, 1e-6)
+        assert same(got, want, f"norm_rope without modulation d={d}")
+
 def test_rope_only_bit_exact(pkg, dev):
     say("apply_rope_split_half fp32 + bf16 tables")
     g = torch.Generator().manual_seed(21)
