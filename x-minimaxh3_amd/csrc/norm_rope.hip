@@ -564,14 +564,31 @@ __global__ __launch_bounds__(1024) void norm_rope_coop_kernel(RowArgs a, int nt)
   // barrier of iteration it, read after that of it + 1, rewritten before that
   // of it + 3).
   //
-  // The folding wave is the row's wave w with w % 4 == 3 where the row has
-  // one: waves are dealt to the CU's four SIMDs in turn, and a block of 15
-  // waves (P = 5, R = 3) leaves SIMD 3 one wave short, so the extra work goes
-  // there (folding on part 0 put it on SIMDs 0-2 and measured 2-3 % slower).
-  // The choice only moves work; any wave of the row gives the same bits.
+  // Folding waves are placed by SIMD load: waves are dealt to the CU's four
+  // SIMDs in turn (wave w on SIMD w % 4), and row by row the fold goes to the
+  // row's wave on the least loaded SIMD, a wave counting 4 and a fold 1. A
+  // block of 15 waves (P = 5, R = 3) leaves SIMD 3 one wave short, and its
+  // three folds all go there (folding on part 0 put them on SIMDs 0-2 and
+  // measured 2-3 % slower); with 12 waves (P = 3, R = 4) the four folds go
+  // to four different SIMDs (107.1 us at 25200 x 3072 against 107.8 us with
+  // all four on SIMD 3: there the spread hardly matters). The choice only
+  // moves work; any wave of the row gives the same bits.
   int par = 0, tsl = 0;
-  const int rp0 = ((3 - sub * P) % 4 + 4) % 4;
-  const int rpart = rp0 < P ? rp0 : 0;
+  int rpart = 0;
+  {
+    // SIMD loads in four scalars (no indexed array, so nothing goes to scratch)
+    const int nw = R * P;
+    int l0 = 4 * ((nw + 3) / 4), l1 = 4 * ((nw + 2) / 4), l2 = 4 * ((nw + 1) / 4), l3 = 4 * (nw / 4);
+    auto load_of = [&](int s) { return s == 0 ? l0 : s == 1 ? l1 : s == 2 ? l2 : l3; };
+    for (int r = 0; r <= sub; ++r) {
+      int best = 0;
+      for (int p = 1; p < P; ++p)
+        if (load_of((r * P + p) & 3) < load_of((r * P + best) & 3)) best = p;
+      const int s = (r * P + best) & 3;
+      l0 += s == 0; l1 += s == 1; l2 += s == 2; l3 += s == 3;
+      rpart = best;
+    }
+  }
   auto front = [&](int it, u32x4 (&bx)[2], u32x4& bt) __attribute__((always_inline)) {
     S* sg = stage + par * 1024;
     const int slot = par * R + sub;
