@@ -263,3 +263,18 @@ def test_segment_rows_resolve_like_tensor_indexing(pkg):
         h3.segment_row_map(10, ((0, 4, -4), (4, 10, 0)), "cpu", n_rows=3)
     with pytest.raises(ValueError, match="ordered partition"):
         h3.segment_row_map(10, ((0, 4, 0), (5, 10, 0)), "cpu", n_rows=3)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with a message and a
+    non-zero status before any device work (no JSON line is printed)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd=root)
+    assert r.returncode != 0
+    assert "one GPU" in r.stdout + r.stderr
+    assert not any(line.startswith("{") for line in r.stdout.splitlines())
