@@ -54,8 +54,8 @@ PEAK_HBM_GBS = 8000.0        # MI355X HBM3E, 8 TB/s
 # 0.5 GiB by FETCH_SIZE and 1 GiB by WRITE_SIZE, so FETCH_SIZE is scaled x2 and
 # WRITE_SIZE x1 (see profiles/).
 TRAFFIC_BYTES = {
-    "fc1_gemm": (1699000.0 * 2 + 680400.0) * 1024,
-    "fc2_gemm": (1481000.0 * 2 + 252000.0) * 1024,
+    "fc1_gemm": (1663720.0 * 2 + 680400.0) * 1024,
+    "fc2_gemm": (1474048.0 * 2 + 252000.0) * 1024,
     "norm_rope": (281245.0 * 2 + 506827.0) * 1024,
 }
 

@@ -381,7 +381,7 @@ static int launch_quant_T(const void* x, int64_t ldx, int64_t M, int64_t K, int8
   const bool vec_ok = (K % 8 == 0) && (ldx % 8 == 0) && (ldq % 8 == 0) &&
                       ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 8 == 0);
   const int64_t steps = (K + 511) / 512;
-  if (vec_ok && steps > 16 && steps <= 32 && M <= (1LL << 24)) {
+  if (vec_ok && steps > 4 && steps <= 32 && M <= (1LL << 24)) {
     constexpr int W = 4;   // waves per row, one row per block
     dim3 grid((unsigned)M);
 #define XMH3_Q2(NLV)                                                                                    \
@@ -390,7 +390,7 @@ static int launch_quant_T(const void* x, int64_t ldx, int64_t M, int64_t K, int8
                        q, ldq, scale, zero_rows);                                                       \
     return check_launch("quant_rows_reg2_kernel");                                                      \
   }
-    XMH3_Q2(5) XMH3_Q2(6) XMH3_Q2(8) XMH3_Q2(10) XMH3_Q2(12) XMH3_Q2(14) XMH3_Q2(16)
+    XMH3_Q2(2) XMH3_Q2(3) XMH3_Q2(4) XMH3_Q2(5) XMH3_Q2(6) XMH3_Q2(8)
 #undef XMH3_Q2
   }
   if (vec_ok && steps <= 32) {
