@@ -64,6 +64,9 @@ def outlier_acts(m, k, seed=0, n_out=8, dtype=torch.bfloat16):
     (999, 13824, torch.bfloat16),    # fc2 width (four waves per row)
     (7, 9000, torch.float16),        # four waves per row, uneven quarters
     (3, 8704, torch.float32),        # four waves per row, fp32 rows
+    (513, 3072, torch.bfloat16),     # four waves per row, two steps each
+    (65, 7680, torch.float16),       # four waves per row, four steps each
+    (9, 11264, torch.bfloat16),      # four waves per row, six steps each
     (37, 1536, torch.float16),
     (33, 520, torch.float32),
     (7, 20000, torch.bfloat16),      # wider than the register path
